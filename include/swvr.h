@@ -1,0 +1,115 @@
+/*
+ * swvr.h — C ABI of the MI355X (gfx950) softmax-weighted embedding readout.
+ *
+ *   S   = logit_scale * h @ W^T + bias          h [N,K], W [V,K], bias [V] (optional)
+ *   O   = softmax(S) @ E                          E [V,D]            -> O   [N,D] fp32
+ *   LSE = logsumexp(S)                                                -> lse [N]   fp32
+ *
+ * and the gradients of (O, LSE) with respect to h, W, E and bias.
+ *
+ * The two compute entry points replace the bodies of the reference's custom ops
+ *   swvr::chunked_fwd   swvr/chunked.py:157-161  (-> _forward,  swvr/chunked.py:82-105)
+ *   swvr::chunked_bwd   swvr/chunked.py:170-178  (-> _backward, swvr/chunked.py:108-151)
+ * The Python autograd.Function of the package calls them through ctypes; see
+ * swvr_amd/_lib.py for the binding.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer on the current HIP device.  The caller
+ *    allocates every output and the workspace; the library never allocates.
+ *  - Work is enqueued on `stream` (a hipStream_t passed as void*); no call
+ *    synchronises the host, except swvr_timing_collect.
+ *  - Row-major operands with unit stride in the last dimension.  h, W and E
+ *    have row strides ldh, ldw, lde (in elements).  K, ldh and ldw must be
+ *    multiples of 8 and h, W 16-byte aligned (the host pads odd K with zero
+ *    columns).  D and lde are unrestricted.
+ *  - The operand dtype (SWVR_BF16, SWVR_F16, SWVR_F32) is the compute dtype of
+ *    the matrix products: the reference's `cdt` (swvr/api.py:8-11).  Products
+ *    accumulate in fp32; scores, softmax state, O and LSE are fp32.
+ *  - Return value: SWVR_OK, or a negative SWVR_E* code; swvr_last_error()
+ *    then holds a message (thread-local).
+ */
+#ifndef SWVR_H_
+#define SWVR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SWVR_ABI_VERSION 1
+
+/* dtype tags */
+#define SWVR_BF16 0
+#define SWVR_F16 1
+#define SWVR_F32 2
+
+/* status codes */
+#define SWVR_OK 0
+#define SWVR_EINVAL (-1)      /* bad shape, stride, alignment or pointer  */
+#define SWVR_EDTYPE (-2)      /* unsupported dtype or D for this dtype    */
+#define SWVR_EHIP (-3)        /* a HIP runtime call failed                */
+#define SWVR_EWORKSPACE (-4)  /* workspace too small                      */
+
+/* Version of this ABI (SWVR_ABI_VERSION).  No reference counterpart. */
+int swvr_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none).
+ * No reference counterpart (the reference raises Python exceptions,
+ * swvr/api.py:14-22). */
+const char* swvr_last_error(void);
+
+/* Largest embedding width D supported for a dtype (256 for bf16/f16, 128 for
+ * f32).  The reference's fused path has the same cap of 256
+ * (swvr/triton_kernels.py:27). */
+int64_t swvr_max_d(int dtype);
+
+/* Workspace bytes swvr_fwd needs for this shape. */
+size_t swvr_fwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D);
+
+/* Forward: O [N,D] (row stride D) and lse [N], both fp32.
+ * Replaces swvr::chunked_fwd (swvr/chunked.py:157-161, 82-105).  bias may be
+ * NULL; it is fp32 [V] and may hold -inf (masked vocabulary).  A row whose
+ * scores are all -inf gets O = NaN and lse = -inf, as the reference does. */
+int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+             const void* h, int64_t ldh, const void* W, int64_t ldw,
+             const void* E, int64_t lde, const float* bias, float logit_scale,
+             float* O, float* lse, void* workspace, size_t workspace_bytes,
+             void* stream);
+
+/* Workspace bytes swvr_bwd needs.  `chunk` is the vocabulary staging chunk
+ * (the reference's chunk_size, swvr/chunked.py:120): the backward stages
+ * dS for `chunk` vocabulary rows at a time, so this is O(N * chunk). */
+size_t swvr_bwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                               int64_t chunk, int need_gh);
+
+/* Backward.  Replaces swvr::chunked_bwd (swvr/chunked.py:170-178, 108-151).
+ * Inputs: the forward's operands, O [N,D] fp32 (row stride D), lse [N] fp32,
+ * gO [N,D] fp32 (row stride D) and glse [N] fp32.
+ * Outputs (any may be NULL = gradient not needed, chunked.py:197-198):
+ *   gh [N,K] (row stride K) in gh_dtype, gW [V,K] (row stride K) in gW_dtype,
+ *   gE [V,D] (row stride D) in gE_dtype, gb [V] fp32.
+ * Gradients are deterministic: no atomics, fixed reduction order. */
+int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+             const void* h, int64_t ldh, const void* W, int64_t ldw,
+             const void* E, int64_t lde, const float* bias, float logit_scale,
+             const float* O, const float* lse, const float* gO, const float* glse,
+             int64_t chunk,
+             void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
+             float* gb, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Instrumentation (no reference counterpart).  While enabled, every kernel
+ * launch is bracketed by a pair of HIP events on its stream.
+ * swvr_timing_collect synchronises those events, writes per-kernel-kind total
+ * milliseconds and launch counts for up to max_kinds kinds, clears the record
+ * and returns the number of kinds.  swvr_kernel_name(kind) names a kind. */
+int swvr_timing_enable(int on);
+int swvr_timing_collect(double* total_ms, int64_t* launches, int max_kinds);
+const char* swvr_kernel_name(int kind);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWVR_H_ */

@@ -1,0 +1,190 @@
+"""Op boundary: the ``swvr::chunked_fwd`` / ``swvr::chunked_bwd`` custom ops.
+
+Mirrors swvr/chunked.py:154-212 of the reference: the forward and backward
+are opaque torch.library custom ops (so torch.compile keeps them whole), with
+fake implementations for tracing and autograd wired through
+``register_autograd``.  Their bodies call the HIP kernels through the C ABI
+(include/swvr.h) on the current stream; there is no other implementation.
+
+The reference op schemas carry a ``use_triton`` flag (chunked.py:157-161,
+170-174); this build has one code path, so the schemas here omit it.
+"""
+from typing import List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+DEFAULT_CHUNK = 8192
+
+
+def acc_dtype(cdt):
+    """Accumulation / output dtype (swvr/chunked.py:26-27): fp32 here, as fp64 is not supported."""
+    return torch.float32
+
+
+def _require_device(t):
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"swvr_amd runs on AMD GPUs through HIP; got a tensor on {t.device}. "
+            "Move h, W, E and bias to the GPU.")
+
+
+def _kpad(K):
+    return (K + 7) // 8 * 8
+
+
+def _matrix(x, cdt, Kp):
+    """``x`` [R, K] in the compute dtype with K padded to Kp, unit inner stride,
+    16-byte aligned rows (the C ABI's alignment contract)."""
+    if x.dtype != cdt:
+        x = x.to(cdt)
+    if x.shape[1] != Kp:
+        x = F.pad(x, (0, Kp - x.shape[1]))
+    if x.stride(1) != 1 or (x.shape[0] > 1 and x.stride(0) % 8 != 0) or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+        if x.data_ptr() % 16 != 0:
+            x = x.clone()
+    return x
+
+
+def _embed(E, cdt):
+    if E.dtype != cdt:
+        E = E.to(cdt)
+    return E if E.stride(1) == 1 else E.contiguous()
+
+
+def _lead_stride(x):
+    return x.stride(0) if x.shape[0] > 1 else x.shape[1]
+
+
+def _forward(h, W, E, bias, logit_scale, chunk, cdt):
+    _require_device(h)
+    lib = _lib.load()
+    if cdt not in _lib.DTYPE_TAG:
+        raise NotImplementedError(f"swvr_amd: compute dtype {cdt} is not supported (bf16, fp16, fp32)")
+    N, K = h.shape
+    V, D = E.shape
+    Kp = _kpad(K)
+    hc, Wc, Ec = _matrix(h, cdt, Kp), _matrix(W, cdt, Kp), _embed(E, cdt)
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    O = torch.empty(N, D, dtype=torch.float32, device=h.device)
+    lse = torch.empty(N, dtype=torch.float32, device=h.device)
+    tag = _lib.DTYPE_TAG[cdt]
+    ws_bytes = lib.swvr_fwd_workspace_size(tag, N, Kp, V, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
+    with torch.cuda.device(h.device):
+        rc = lib.swvr_fwd(tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc), _lead_stride(Wc),
+                          _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
+                          _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_of(h.device))
+    _lib.check(rc)
+    return O, lse
+
+
+def _grad_buffer(shape, want, device):
+    """Buffer the kernels write a gradient into: the parameter's own dtype when
+    the ABI has a tag for it, else fp32 (cast afterwards)."""
+    dt = want if want in _lib.DTYPE_TAG else torch.float32
+    return torch.empty(shape, dtype=dt, device=device)
+
+
+def _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, need_W, need_E, need_b):
+    _require_device(h)
+    lib = _lib.load()
+    N, K = h.shape
+    V, D = E.shape
+    Kp = _kpad(K)
+    hc, Wc, Ec = _matrix(h, cdt, Kp), _matrix(W, cdt, Kp), _embed(E, cdt)
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    dev = h.device
+    gh = _grad_buffer((N, Kp), h.dtype, dev) if need_h else None
+    gW = _grad_buffer((V, Kp), W.dtype, dev) if need_W else None
+    gE = _grad_buffer((V, D), E.dtype, dev) if need_E else None
+    gb = torch.empty(V, dtype=torch.float32, device=dev) if need_b else None
+    gO32 = gO.to(torch.float32).contiguous()
+    glse32 = glse.to(torch.float32).contiguous()
+    O32 = O.to(torch.float32).contiguous()
+    lse32 = lse.to(torch.float32).contiguous()
+    tag = _lib.DTYPE_TAG[cdt]
+    ws_bytes = lib.swvr_bwd_workspace_size(tag, N, Kp, V, D, int(chunk), int(need_h))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def tag_of(t):
+        return _lib.DTYPE_TAG[t.dtype] if t is not None else 0
+
+    with torch.cuda.device(dev):
+        rc = lib.swvr_bwd(tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc), _lead_stride(Wc),
+                          _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
+                          _lib.ptr(O32), _lib.ptr(lse32), _lib.ptr(gO32), _lib.ptr(glse32), int(chunk),
+                          _lib.ptr(gh), tag_of(gh), _lib.ptr(gW), tag_of(gW), _lib.ptr(gE), tag_of(gE),
+                          _lib.ptr(gb), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
+    _lib.check(rc)
+    if gh is not None:
+        gh = gh[:, :K] if Kp != K else gh
+        gh = gh.to(h.dtype) if gh.dtype != h.dtype else gh
+    if gW is not None:
+        gW = gW[:, :K].contiguous() if Kp != K else gW
+        gW = gW.to(W.dtype) if gW.dtype != W.dtype else gW
+    if gE is not None and gE.dtype != E.dtype:
+        gE = gE.to(E.dtype)
+    if gb is not None and gb.dtype != bias.dtype:
+        gb = gb.to(bias.dtype)
+    return gh, gW, gE, gb
+
+
+@torch.library.custom_op("swvr::chunked_fwd", mutates_args=())
+def _fwd_op(h: torch.Tensor, W: torch.Tensor, E: torch.Tensor, bias: Optional[torch.Tensor],
+            logit_scale: float, chunk: int, cdt: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _forward(h, W, E, bias, logit_scale, chunk, cdt)
+
+
+@_fwd_op.register_fake
+def _(h, W, E, bias, logit_scale, chunk, cdt):
+    adt = acc_dtype(cdt)
+    return h.new_empty(h.shape[0], E.shape[1], dtype=adt), h.new_empty(h.shape[0], dtype=adt)
+
+
+@torch.library.custom_op("swvr::chunked_bwd", mutates_args=())
+def _bwd_op(gO: torch.Tensor, glse: torch.Tensor, h: torch.Tensor, W: torch.Tensor, E: torch.Tensor,
+            bias: Optional[torch.Tensor], O: torch.Tensor, lse: torch.Tensor, logit_scale: float,
+            chunk: int, cdt: torch.dtype, need_h: bool, need_W: bool, need_E: bool,
+            need_b: bool) -> List[torch.Tensor]:
+    grads = _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt,
+                      need_h, need_W, need_E, need_b)
+    # a custom op cannot return None: an empty tensor stands for "no gradient"
+    return [g if g is not None else h.new_empty(0) for g in grads]
+
+
+@_bwd_op.register_fake
+def _(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, need_W, need_E, need_b):
+    like = [(need_h, h), (need_W, W), (need_E, E), (need_b, bias)]
+    return [torch.empty_like(x) if need else h.new_empty(0) for need, x in like]
+
+
+def _setup_context(ctx, inputs, output):
+    h, W, E, bias, logit_scale, chunk, cdt = inputs
+    O, lse = output
+    ctx.save_for_backward(h, W, E, bias, O, lse)
+    ctx.args = (logit_scale, chunk, cdt)
+
+
+def _autograd_backward(ctx, gO, glse):
+    h, W, E, bias, O, lse = ctx.saved_tensors
+    needs = [bool(n) for n in ctx.needs_input_grad[:4]]
+    needs[3] = needs[3] and bias is not None
+    gO = gO if gO is not None else torch.zeros_like(O)
+    glse = glse if glse is not None else torch.zeros_like(lse)
+    grads = _bwd_op(gO, glse, h, W, E, bias, O, lse, *ctx.args, *needs)
+    return (*[g if need else None for g, need in zip(grads, needs)], None, None, None)
+
+
+_fwd_op.register_autograd(_autograd_backward, setup_context=_setup_context)
+
+
+def softmax_readout_op(h2, W, E, bias, logit_scale, chunk, cdt):
+    """``h2`` is ``[N, K]``; returns ``(O [N, D], LSE [N])`` in fp32 (swvr/chunked.py:208-212)."""
+    if h2.device.type not in ("cuda", "cpu"):  # meta / fake tracing: no autocast state
+        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)
+    with torch.autocast(h2.device.type, enabled=False):
+        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)

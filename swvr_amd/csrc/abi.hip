@@ -1,0 +1,248 @@
+// C ABI entry points (include/swvr.h): argument checks, error reporting,
+// launch timing, and dispatch to the forward / backward launchers.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/swvr.h"
+#include "launch.hpp"
+
+namespace swvr {
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SWVR_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+// ---- launch timing: event pairs per kernel kind, recorded on the launch stream
+struct TimedLaunch {
+  int kind;
+  hipEvent_t start, stop;
+};
+std::mutex g_tmu;
+bool g_timing = false;
+std::vector<TimedLaunch> g_launches;
+std::vector<hipEvent_t> g_pool;
+hipEvent_t g_pending[kNumKinds];
+
+hipEvent_t take_event() {
+  if (!g_pool.empty()) {
+    hipEvent_t e = g_pool.back();
+    g_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",  "fwd_combine_kernel", "bwd_delta_kernel",
+                                     "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
+                                     "fill_zero_kernel"};
+
+bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
+                 int64_t ldw, const void* E, int64_t lde) {
+  if (!is_dtype(dtype)) return fail(SWVR_EDTYPE, "unsupported operand dtype tag %d", dtype);
+  if (N < 0 || K < 0 || V < 0 || D < 0) return fail(SWVR_EINVAL, "negative size N=%lld K=%lld V=%lld D=%lld",
+                                                    (long long)N, (long long)K, (long long)V, (long long)D);
+  if (N > INT32_MAX || K > INT32_MAX || V > INT32_MAX || D > INT32_MAX)
+    return fail(SWVR_EINVAL, "sizes must fit in 32 bits");
+  if (D > swvr_max_d(dtype))
+    return fail(SWVR_EDTYPE, "D=%lld exceeds the maximum %lld for this dtype", (long long)D,
+                (long long)swvr_max_d(dtype));
+  if (K % 8 != 0) return fail(SWVR_EINVAL, "K=%lld must be a multiple of 8 (pad h and W)", (long long)K);
+  if (ldh < K || ldh % 8 != 0) return fail(SWVR_EINVAL, "ldh=%lld must be >= K and a multiple of 8", (long long)ldh);
+  if (ldw < K || ldw % 8 != 0) return fail(SWVR_EINVAL, "ldw=%lld must be >= K and a multiple of 8", (long long)ldw);
+  if (lde < D) return fail(SWVR_EINVAL, "lde=%lld must be >= D", (long long)lde);
+  if (N > 0 && K > 0 && (!h || !aligned16(h))) return fail(SWVR_EINVAL, "h must be a non-null 16-byte aligned pointer");
+  if (V > 0 && K > 0 && (!W || !aligned16(W))) return fail(SWVR_EINVAL, "W must be a non-null 16-byte aligned pointer");
+  if (V > 0 && D > 0 && !E) return fail(SWVR_EINVAL, "E must be non-null");
+  return SWVR_OK;
+}
+
+}  // namespace
+
+void timing_begin(int kind, hipStream_t stream) {
+  if (!g_timing) return;
+  std::lock_guard<std::mutex> lk(g_tmu);
+  hipEvent_t e = take_event();
+  if (e && hipEventRecord(e, stream) == hipSuccess) g_pending[kind] = e;
+}
+
+void timing_end(int kind, hipStream_t stream) {
+  if (!g_timing) return;
+  std::lock_guard<std::mutex> lk(g_tmu);
+  hipEvent_t s = g_pending[kind];
+  g_pending[kind] = nullptr;
+  if (!s) return;
+  hipEvent_t e = take_event();
+  if (e && hipEventRecord(e, stream) == hipSuccess) g_launches.push_back({kind, s, e});
+}
+
+}  // namespace swvr
+
+using namespace swvr;
+
+extern "C" {
+
+int swvr_abi_version(void) { return SWVR_ABI_VERSION; }
+
+const char* swvr_last_error(void) { return g_err; }
+
+int64_t swvr_max_d(int dtype) {
+  if (dtype == SWVR_F32) return 128;
+  if (dtype == SWVR_BF16 || dtype == SWVR_F16) return 256;
+  return 0;
+}
+
+size_t swvr_fwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D) {
+  FwdPlan plan;
+  if (N < 0 || V < 0 || D < 0 || !fwd_plan(dtype, N, K, V, D, &plan)) return 0;
+  return plan.ws_bytes;
+}
+
+int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
+             int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, float* O, float* lse,
+             void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
+  if (rc != SWVR_OK) return rc;
+  if (N > 0 && ((D > 0 && !O) || !lse)) return fail(SWVR_EINVAL, "O and lse must be non-null");
+  FwdPlan plan;
+  if (!fwd_plan(dtype, N, K, V, D, &plan)) return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (N == 0) return SWVR_OK;
+  if (!workspace || workspace_bytes < plan.ws_bytes)
+    return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+  FwdParams p;
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  char* ws = static_cast<char*>(workspace);
+  const size_t per = (size_t)N * sizeof(float);
+  p.part_m = reinterpret_cast<float*>(ws);
+  p.part_l = reinterpret_cast<float*>(ws + plan.n_part * per);
+  p.part_acc = reinterpret_cast<float*>(ws + 2 * plan.n_part * per);
+  hipError_t e = fwd_launch(dtype, plan, p, O, lse, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return SWVR_OK;
+}
+
+size_t swvr_bwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, int need_gh) {
+  BwdPlan plan;
+  if (N < 0 || V < 0 || D < 0 || chunk <= 0 || !bwd_plan(dtype, N, K, V, D, chunk, need_gh != 0, &plan)) return 0;
+  return plan.ws_bytes;
+}
+
+int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
+             int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, const float* O,
+             const float* lse, const float* gO, const float* glse, int64_t chunk, void* gh, int gh_dtype, void* gW,
+             int gW_dtype, void* gE, int gE_dtype, float* gb, void* workspace, size_t workspace_bytes,
+             void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
+  if (rc != SWVR_OK) return rc;
+  if (chunk <= 0) return fail(SWVR_EINVAL, "chunk must be positive, got %lld", (long long)chunk);
+  if (gh && !is_dtype(gh_dtype)) return fail(SWVR_EDTYPE, "unsupported gh dtype tag %d", gh_dtype);
+  if (gW && !is_dtype(gW_dtype)) return fail(SWVR_EDTYPE, "unsupported gW dtype tag %d", gW_dtype);
+  if (gE && !is_dtype(gE_dtype)) return fail(SWVR_EDTYPE, "unsupported gE dtype tag %d", gE_dtype);
+  if (gb && !bias) return fail(SWVR_EINVAL, "gb requested without a bias");
+  if (N > 0 && (!lse || !glse || (D > 0 && (!O || !gO)))) return fail(SWVR_EINVAL, "O, lse, gO and glse must be non-null");
+  BwdPlan plan;
+  if (!bwd_plan(dtype, N, K, V, D, chunk, gh != nullptr, &plan))
+    return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (N > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
+    return fail(SWVR_EWORKSPACE, "backward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+  BwdParams p;
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  p.O = O;
+  p.lse = lse;
+  p.gO = gO;
+  p.glse = glse;
+  p.gh = gh;
+  p.gh_dtype = gh_dtype;
+  p.gW = gW;
+  p.gW_dtype = gW_dtype;
+  p.gE = gE;
+  p.gE_dtype = gE_dtype;
+  p.gb = gb;
+  p.ws = static_cast<char*>(workspace);
+  hipError_t e = bwd_launch(dtype, plan, p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "backward launch");
+  return SWVR_OK;
+}
+
+int swvr_timing_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  g_timing = on != 0;
+  return SWVR_OK;
+}
+
+int swvr_timing_collect(double* total_ms, int64_t* launches, int max_kinds) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  std::vector<double> ms(kNumKinds, 0.0);
+  std::vector<int64_t> cnt(kNumKinds, 0);
+  int rc = SWVR_OK;
+  for (const TimedLaunch& t : g_launches) {
+    hipError_t e = hipEventSynchronize(t.stop);
+    float f = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&f, t.start, t.stop);
+    if (e != hipSuccess && rc == SWVR_OK) rc = hip_fail(e, "timing event");
+    ms[t.kind] += f;
+    cnt[t.kind] += 1;
+    g_pool.push_back(t.start);
+    g_pool.push_back(t.stop);
+  }
+  g_launches.clear();
+  if (rc != SWVR_OK) return rc;
+  const int n = max_kinds < kNumKinds ? max_kinds : kNumKinds;
+  for (int k = 0; k < n; ++k) {
+    if (total_ms) total_ms[k] = ms[k];
+    if (launches) launches[k] = cnt[k];
+  }
+  return kNumKinds;
+}
+
+const char* swvr_kernel_name(int kind) {
+  if (kind < 0 || kind >= kNumKinds) return "";
+  return kKindNames[kind];
+}
+
+}  // extern "C"

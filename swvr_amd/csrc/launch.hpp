@@ -1,0 +1,96 @@
+// Host-side interface between the C ABI (abi.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace swvr {
+
+// Kernel kinds, for the launch timing record.
+enum KernelKind {
+  kKindFwdTile = 0,
+  kKindFwdCombine,
+  kKindBwdDelta,
+  kKindBwdScores,
+  kKindBwdGemm,
+  kKindBwdReduce,
+  kKindFill,
+  kNumKinds
+};
+
+// Timing hooks (abi.hip): bracket one launch when timing is enabled.
+void timing_begin(int kind, hipStream_t stream);
+void timing_end(int kind, hipStream_t stream);
+
+// ---------------------------------------------------------------- forward
+struct FwdParams {
+  const void* h;
+  int64_t ldh;
+  const void* W;
+  int64_t ldw;
+  const void* E;
+  int64_t lde;
+  const float* bias;  // fp32 [V] or null
+  float scale;
+  int N, K, V, D;
+  int n_tb, n_split, n_vt;
+  float* part_m;    // [n_part][N]
+  float* part_l;    // [n_part][N]
+  float* part_acc;  // [n_part][DP][N]
+};
+
+struct FwdPlan {
+  int BV, BM, DP;
+  int n_tb, n_vt, n_split, n_part;
+  size_t ws_bytes;
+};
+
+// Tile shape, split count and workspace for a forward call; ok=false if the
+// dtype / D combination is unsupported.
+bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan);
+hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, float* O, float* lse, hipStream_t stream);
+
+// ---------------------------------------------------------------- backward
+struct BwdPlan {
+  int DP;
+  int BM, BV;            // dS kernel tile: BM tokens x BV vocabulary
+  int GM, GN;            // gradient GEMM tile
+  int n_tb;              // token blocks of the dS kernel
+  int64_t N_pad;         // token stride of the dS stage
+  int64_t C;             // vocabulary rows per chunk (multiple of BV)
+  int n_chunks;
+  int G;                 // token groups of the dS kernel (dE / db partials)
+  bool dh_acc;           // dh needs an fp32 accumulator across chunks
+  size_t off_delta, off_stage, off_pe, off_pb, off_dh, ws_bytes;
+};
+
+bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
+              BwdPlan* plan);
+
+struct BwdParams {
+  const void* h;
+  int64_t ldh;
+  const void* W;
+  int64_t ldw;
+  const void* E;
+  int64_t lde;
+  const float* bias;
+  float scale;
+  int N, K, V, D;
+  const float* O;
+  const float* lse;
+  const float* gO;
+  const float* glse;
+  void* gh;
+  int gh_dtype;
+  void* gW;
+  int gW_dtype;
+  void* gE;
+  int gE_dtype;
+  float* gb;
+  char* ws;
+};
+
+hipError_t bwd_launch(int dtype, const BwdPlan& plan, const BwdParams& p, hipStream_t stream);
+
+}  // namespace swvr

@@ -1,0 +1,235 @@
+"""The reference's CPU test behaviours (tests/test_cpu.py) run through the HIP path.
+
+The reference checks these in fp64 on the CPU; this build has no CPU path and
+its fp64 is not supported, so they run in fp32 on the GPU against the fp64
+oracle with fp32-sized tolerances, plus the golden fixtures.
+"""
+import json
+import os
+
+import pytest
+import torch
+from torch import nn
+
+import swvr_amd as swvr
+from oracle import reference as ref
+from tests.gpu_util import rel_err
+
+pytestmark = pytest.mark.gpu
+f32, f64 = torch.float32, torch.float64
+TOL = dict(rtol=2e-5, atol=2e-5)
+
+
+def make(N=6, K=12, V=41, D=5, dtype=f32, bias=True, lead=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    shape = (*(lead or (N,)), K)
+    t = lambda *s: torch.randn(*s, generator=g, dtype=f64).to(device="cuda", dtype=dtype)
+    h, W, E = t(*shape), t(V, K), t(V, D)
+    b = t(V) if bias else None
+    for x in (h, W, E, b):
+        if x is not None:
+            x.requires_grad_(True)
+    return h, W, E, b
+
+
+def grads(fn, inputs, seed=1):
+    outs = fn(*inputs)
+    g = torch.Generator().manual_seed(seed)
+    loss = sum((o * torch.randn(o.shape, generator=g, dtype=f64).to(o)).sum() for o in outs)
+    xs = [x for x in inputs if x is not None and x.requires_grad]
+    return outs, torch.autograd.grad(loss, xs, allow_unused=True)
+
+
+def oracle_grads(inputs, scale=1.0, seed=1):
+    """fp64 CPU copies that keep tied inputs tied (the same tensor passed twice)."""
+    copies = {}
+    for x in inputs:
+        if x is not None and id(x) not in copies:
+            copies[id(x)] = x.detach().cpu().double().requires_grad_(x.requires_grad)
+    cpu = [copies[id(x)] if x is not None else None for x in inputs]
+    return grads(lambda *a: ref.softmax_readout_reference(*a, logit_scale=scale), cpu, seed)
+
+
+def assert_matches_oracle(h, W, E, b, scale=1.0, chunk=8, tol=TOL):
+    (o1, g1) = grads(lambda *a: swvr.softmax_readout(*a, logit_scale=scale, chunk_size=chunk), (h, W, E, b))
+    (o2, g2) = oracle_grads((h, W, E, b), scale)
+    for a, r in zip(o1, o2):
+        torch.testing.assert_close(a.double().cpu(), r, **tol)
+    for a, r in zip(g1, g2):
+        torch.testing.assert_close(a.double().cpu(), r, **tol)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 8, 40, 41, 42, 1000])
+def test_chunk_sizes_match_oracle(chunk):
+    assert_matches_oracle(*make(), chunk=chunk)
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("scale", [1.0, 0.3, 2.5])
+def test_scales_and_bias(bias, scale):
+    assert_matches_oracle(*make(N=4, K=6, V=13, D=3, bias=bias), scale=scale, chunk=5)
+
+
+def test_leading_dims():
+    h, W, E, b = make(lead=(2, 3, 4))
+    O, lse = swvr.softmax_readout(h, W, E, b, chunk_size=7)
+    assert O.shape == (2, 3, 4, 5) and lse.shape == (2, 3, 4)
+    assert_matches_oracle(h, W, E, b)
+
+
+def test_non_contiguous_h():
+    h, W, E, b = make(N=8)
+    h_t = h.detach().t().contiguous().t()[::2].requires_grad_(True)
+    assert not h_t.is_contiguous()
+    assert_matches_oracle(h_t, W, E, b)
+
+
+def test_empty_batch():
+    h, W, E, b = make(N=0)
+    O, lse = swvr.softmax_readout(h, W, E, b, chunk_size=8)
+    assert O.shape == (0, 5) and lse.shape == (0,)
+    (O.sum() + lse.sum()).backward()
+    assert W.grad.abs().sum() == 0 and E.grad.abs().sum() == 0 and b.grad.abs().sum() == 0
+
+
+def test_single_token_and_tiny_vocab():
+    assert_matches_oracle(*make(N=1, V=1), chunk=8)
+    assert_matches_oracle(*make(N=1, V=2), chunk=1)
+
+
+def test_large_logits_no_overflow():
+    h, W, E, b = make()
+    with torch.no_grad():
+        b[3] = 1e4
+        b[7] = -1e4
+    assert_matches_oracle(h, W, E, b)
+    O, _ = swvr.softmax_readout(h, W, E, b, chunk_size=8)
+    torch.testing.assert_close(O, E[3].expand_as(O).detach())
+
+
+def test_masked_vocab_with_neg_inf_bias():
+    h, W, E, b = make(V=40)
+    with torch.no_grad():
+        b[:16] = float("-inf")
+        b[30:] = float("-inf")
+    O, lse = swvr.softmax_readout(h, W, E, b, chunk_size=8)
+    cpu = [x.detach().cpu().double() for x in (h, W, E, b)]
+    O_r, lse_r = ref.softmax_readout_reference(*cpu)
+    torch.testing.assert_close(O.double().cpu(), O_r, **TOL)
+    torch.testing.assert_close(lse.double().cpu(), lse_r, **TOL)
+    (_, gs) = grads(lambda *a: swvr.softmax_readout(*a, chunk_size=8), (h, W, E, b))
+    (_, gs_r) = oracle_grads((h, W, E, b))
+    for a, r in zip(gs, gs_r):
+        torch.testing.assert_close(a.double().cpu(), r, **TOL)
+    assert (gs[3][:16] == 0).all() and (gs[3][30:] == 0).all()
+
+
+def test_fully_masked_row_matches_reference_nan():
+    h, W, E, b = make(V=10)
+    with torch.no_grad():
+        b[:] = float("-inf")
+    O, lse = swvr.softmax_readout(h, W, E, b)
+    assert torch.isnan(O).all() and torch.isneginf(lse).all()
+
+
+@pytest.mark.parametrize("frozen", ["h", "W", "E", "b", "WE"])
+def test_frozen_inputs(frozen):
+    h, W, E, b = make()
+    names = dict(h=h, W=W, E=E, b=b)
+    for k in frozen:
+        names[k].requires_grad_(False)
+    assert_matches_oracle(h, W, E, b)
+
+
+def test_tied_W_and_E():
+    h, W, _, b = make(K=7, D=7)
+    assert_matches_oracle(h, W, W, b)
+
+
+def test_only_lse_or_only_O_used():
+    h, W, E, b = make()
+    cpu = [x.detach().cpu().double().requires_grad_(True) for x in (h, W, E, b)]
+    for pick in (0, 1):
+        out = swvr.softmax_readout(h, W, E, b, chunk_size=8)[pick].sum()
+        want = ref.softmax_readout_reference(*cpu)[pick].sum()
+        g = torch.autograd.grad(out, (h, W, E, b), allow_unused=True)
+        gr = torch.autograd.grad(want, cpu, allow_unused=True)
+        for a, r in zip(g, gr):
+            if r is None:
+                assert a is None or a.abs().max() == 0
+            else:
+                torch.testing.assert_close(a.double().cpu(), r, **TOL)
+
+
+def test_bf16_inputs_return_fp32():
+    h, W, E, b = make(dtype=torch.bfloat16, K=32, V=300)
+    O, lse = swvr.softmax_readout(h, W, E, b, chunk_size=64)
+    assert O.dtype == f32 and lse.dtype == f32
+    O_r, lse_r = ref.softmax_readout_reference(*(x.detach().cpu().double() for x in (h, W, E, b)))
+    torch.testing.assert_close(lse.double().cpu(), lse_r, rtol=1e-3, atol=1e-2)
+    torch.testing.assert_close(O.double().cpu(), O_r, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_mse_matches_oracle(reduction):
+    h, W, E, b = make(lead=(2, 3))
+    target = torch.randn(2, 3, 5, dtype=f64).cuda().float()
+    weight = torch.tensor([[1., 0., 2.], [1., 1., 0.]], device="cuda")
+    kw = dict(weight=weight, reduction=reduction, z_loss_weight=0.1, logit_scale=0.5)
+    loss = swvr.softmax_readout_mse(h, W, E, target, b, chunk_size=8, **kw)
+    cpu = [x.detach().cpu().double().requires_grad_(True) for x in (h, W, E, b)]
+    kwc = dict(kw, weight=weight.cpu().double())
+    want = ref.mse_reference(cpu[0], cpu[1], cpu[2], target.cpu().double(), cpu[3], **kwc)
+    torch.testing.assert_close(loss.double().cpu(), want, **TOL)
+    g = torch.autograd.grad(loss.sum(), (h, W, E, b))
+    gr = torch.autograd.grad(want.sum(), cpu)
+    for a, r in zip(g, gr):
+        torch.testing.assert_close(a.double().cpu(), r, **TOL)
+
+
+def test_module_wraps_linear_and_embedding():
+    torch.manual_seed(0)
+    head, emb = nn.Linear(12, 41).cuda(), nn.Embedding(41, 5).cuda()
+    h, target = torch.randn(7, 12, device="cuda"), torch.randn(7, 5, device="cuda")
+    loss_fn = swvr.SoftmaxReadoutMSE(head, emb, z_loss_weight=1e-2, chunk_size=8)
+    loss = loss_fn(h, target)
+    cpu = [p.detach().cpu().double() for p in (head.weight, emb.weight, head.bias)]
+    want = ref.mse_reference(h.cpu().double(), cpu[0], cpu[1], target.cpu().double(), cpu[2], z_loss_weight=1e-2)
+    torch.testing.assert_close(loss.double().cpu(), want, **TOL)
+    loss.backward()
+    assert head.weight.grad is not None and head.bias.grad is not None and emb.weight.grad is not None
+
+
+def test_activation_checkpointing():
+    from torch.utils.checkpoint import checkpoint
+    h, W, E, b = make()
+    fn = lambda h: swvr.softmax_readout(h, W, E, b, chunk_size=8)[0].pow(2).sum()
+    g1 = torch.autograd.grad(checkpoint(fn, h, use_reentrant=False), h)[0]
+    g2 = torch.autograd.grad(fn(h), h)[0]
+    torch.testing.assert_close(g1, g2)
+
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "readout_cases.json")))["cases"]
+
+
+@pytest.mark.parametrize("case", GOLD, ids=[c["name"] for c in GOLD])
+def test_golden_fixtures_through_hip_fp32(case):
+    c = case
+    t = lambda x: None if x is None else torch.tensor(x, dtype=f32, device="cuda")
+    xs = [t(c[k]) for k in ("h", "W", "E", "bias")]
+    xs = [x.requires_grad_(True) if x is not None else None for x in xs]
+    O, lse = swvr.softmax_readout(*xs, logit_scale=c["logit_scale"], chunk_size=3)
+    gO, glse = t(c["gO"]), t(c["glse"])
+    want_in = [x for x in xs if x is not None]
+    gs = torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), want_in)
+    got = dict(O=O, lse=lse, gh=gs[0], gW=gs[1], gE=gs[2], gb=gs[3] if len(gs) > 3 else None)
+    for k, v in got.items():
+        if c[k] is None:
+            continue
+        want = torch.tensor(c[k], dtype=f64)
+        assert rel_err(v, want) < 1e-5, (k, rel_err(v, want))
+    if "mse" in c:
+        kw = dict(weight=t(c["weight"]), z_loss_weight=c["z_loss_weight"], logit_scale=c["logit_scale"])
+        for red, want in c["mse"].items():
+            got = swvr.softmax_readout_mse(*xs[:3], t(c["target"]), xs[3], reduction=red, **kw)
+            assert rel_err(got, torch.tensor(want, dtype=f64)) < 1e-5

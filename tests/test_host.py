@@ -1,0 +1,169 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every
+symbol include/swvr.h declares, its argument checks report errors without
+touching the device, and the Python API validates, traces and refuses CPU
+tensors the way the reference's does (swvr/api.py:14-22, 37-39)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import swvr_amd
+from swvr_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "swvr.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(swvr_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 10, names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "binding and header disagree"
+
+
+def test_abi_constants():
+    lib = _lib.load()
+    assert lib.swvr_abi_version() == _lib.ABI_VERSION
+    assert lib.swvr_max_d(_lib.BF16) == 256 and lib.swvr_max_d(_lib.F16) == 256
+    assert lib.swvr_max_d(_lib.F32) == 128 and lib.swvr_max_d(9) == 0
+    assert lib.swvr_kernel_name(0).decode() == "fwd_tile_kernel"
+    assert lib.swvr_kernel_name(99) == b""
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    N, K, V, D = 16384, 2560, 151936, 64
+    fwd = lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, D)
+    assert 0 < fwd < 2**30
+    bwd = lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 8192, 1)
+    # dS stage (N x 8192 bf16) + fp32 dh accumulator + small partials: O(N * chunk + N * K)
+    assert N * 8192 * 2 + N * K * 4 <= bwd < N * 8192 * 2 + N * K * 4 + 2**27
+    assert lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 0, 1) == 0
+    assert lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 256) == 0   # fp32 caps D at 128
+
+
+def call_fwd(dtype=_lib.BF16, N=4, K=16, V=8, D=4, h=16, ldh=16, W=16, ldw=16, E=16, lde=4):
+    lib = _lib.load()
+    p = lambda x: ctypes.c_void_p(x) if x else None
+    return lib.swvr_fwd(dtype, N, K, V, D, p(h), ldh, p(W), ldw, p(E), lde, None, 1.0,
+                        p(16), p(16), p(16), 1 << 20, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), _lib.EDTYPE),
+    (dict(K=12, ldh=12, ldw=12), _lib.EINVAL),      # K must be a multiple of 8
+    (dict(ldh=8), _lib.EINVAL),                     # ldh < K
+    (dict(h=8), _lib.EINVAL),                       # misaligned h
+    (dict(W=0), _lib.EINVAL),                       # null W
+    (dict(D=300, lde=300), _lib.EDTYPE),            # D above the bf16 cap
+    (dict(dtype=_lib.F32, D=200, lde=200), _lib.EDTYPE),
+    (dict(N=-1), _lib.EINVAL),
+])
+def test_abi_rejects_bad_arguments_without_touching_the_device(kw, code):
+    assert call_fwd(**kw) == code
+    assert _lib.load().swvr_last_error()
+
+
+def test_abi_bwd_rejects_bad_chunk_and_gradient_dtype():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    args = [_lib.BF16, 4, 16, 8, 4, p, 16, p, 16, p, 4, None, 1.0, p, p, p, p]
+    rc = lib.swvr_bwd(*args, 0, p, _lib.BF16, None, 0, None, 0, None, p, 1 << 20, None)
+    assert rc == _lib.EINVAL and b"chunk" in lib.swvr_last_error()
+    rc = lib.swvr_bwd(*args, 64, p, 5, None, 0, None, 0, None, p, 1 << 20, None)
+    assert rc == _lib.EDTYPE
+    rc = lib.swvr_bwd(*args, 64, None, 0, None, 0, None, 0, p, p, 1 << 20, None)
+    assert rc == _lib.EINVAL and b"bias" in lib.swvr_last_error()
+
+
+def test_check_maps_codes_to_exceptions():
+    lib = _lib.load()
+    call_fwd(K=12, ldh=12, ldw=12)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EINVAL)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.EDTYPE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.EHIP)
+    _lib.check(_lib.OK)
+    assert lib is _lib.load()
+
+
+def make(N=6, K=12, V=41, D=5, device="cpu", dtype=torch.float32):
+    g = torch.Generator().manual_seed(0)
+    t = lambda *s: torch.randn(*s, generator=g).to(device=device, dtype=dtype)
+    return t(N, K), t(V, K), t(V, D), t(V)
+
+
+def test_input_validation_matches_reference():
+    h, W, E, b = make()
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout(h, W[:, :-1], E)
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout(h, W, E[:-1])
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout(h, W, E, b[:-1])
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout(h, W, E, chunk_size=-1)
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout(h, W[None], E)
+    hm, Wm, Em, bm = make(device="meta")
+    with pytest.raises(ValueError):
+        swvr_amd.softmax_readout_mse(hm, Wm, Em, torch.zeros(6, 5, device="meta"), bm, reduction="max")
+
+
+def test_cpu_tensors_fail_loudly():
+    h, W, E, b = make()
+    with pytest.raises(RuntimeError, match="GPU"):
+        swvr_amd.softmax_readout(h, W, E, b)
+
+
+def test_meta_tensors_trace_through_the_fake_kernels():
+    h, W, E, b = make(device="meta")
+    h = h.reshape(2, 3, 12)
+    O, lse = swvr_amd.softmax_readout(h, W, E, b)
+    assert O.shape == (2, 3, 5) and lse.shape == (2, 3)
+    assert O.dtype == torch.float32 and lse.dtype == torch.float32
+    hb, Wb, Eb, bb = (x.to(torch.bfloat16) for x in make(device="meta"))
+    O, lse = swvr_amd.softmax_readout(hb, Wb, Eb, bb)
+    assert O.dtype == torch.float32   # scores, O and LSE stay fp32 for bf16 inputs
+    grads = torch.ops.swvr.chunked_bwd(torch.empty(6, 5, device="meta"), torch.empty(6, device="meta"),
+                                       hb, Wb, Eb, bb, O, lse, 1.0, 8, torch.bfloat16, True, False, True, True)
+    assert [tuple(g.shape) for g in grads] == [(6, 12), (0,), (41, 5), (41,)]
+    assert grads[0].dtype == torch.bfloat16
+
+
+def test_drop_in_alias():
+    import swvr
+    assert swvr.softmax_readout is swvr_amd.softmax_readout
+    assert swvr.softmax_readout_mse is swvr_amd.softmax_readout_mse
+    assert swvr.SoftmaxReadoutMSE is swvr_amd.SoftmaxReadoutMSE
+    assert swvr.softmax_readout_reference is swvr_amd.softmax_readout_reference
+    assert set(swvr.__all__) == {"softmax_readout", "softmax_readout_mse", "SoftmaxReadoutMSE",
+                                 "softmax_readout_reference"}
+
+
+def test_public_reference_matches_oracle():
+    from oracle import reference as ref
+    h, W, E, b = (x.double() for x in make())
+    a = swvr_amd.softmax_readout_reference(h, W, E, b, logit_scale=0.5)
+    r = ref.softmax_readout_reference(h, W, E, b, logit_scale=0.5)
+    for x, y in zip(a, r):
+        torch.testing.assert_close(x, y)
+
+
+def test_default_chunk_size_env(monkeypatch):
+    monkeypatch.delenv("SWVR_CHUNK", raising=False)
+    assert swvr_amd.default_chunk_size() == 8192
+    monkeypatch.setenv("SWVR_CHUNK", "4096")
+    assert swvr_amd.default_chunk_size() == 4096
