@@ -1,0 +1,215 @@
+"""Benchmark: fwd+bwd of swvr_amd.softmax_readout_mse on one MI355X.
+
+    python bench.py                      # headline (config 3), 10 timed steps
+    python bench.py --config 2 --steps 20 --warmup 3
+    python bench.py --no-cpu             # skip the CPU baseline leg
+
+A step is one forward + backward of the MSE loss (the reference's bench,
+bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
+Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd TFLOP/s,
+2 N V (4K + 3D) / step time — the FLOPs of the reference's algorithm with one
+score recompute (docs/DESIGN.md:39); ``ms_per_step`` is the step time.
+
+The dominant kernel's roofline is measured live: every launch in the timed
+region is bracketed by HIP events on its own stream (the C ABI's timing
+record), and its average duration is priced against its algorithmic FLOPs.
+The CPU baseline times this repository's restatement of the reference's
+chunked CPU path (oracle/chunked.py) on the host cores, on a token sample of
+the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd ms, TFLOP/s & % bf16 MFMA peak at N16k K2560 V152k D64; peak GiB"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
+PEAK_HBM_GBS = 8000.0
+
+# BASELINE.json configs (2-5 run on the GPU; config 1 is the CPU plumbing case)
+CONFIGS = {
+    2: dict(N=16384, K=1024, V=151936, D=16, bias=False, weight=None, z=0.0),
+    3: dict(N=16384, K=2560, V=151936, D=64, bias=True, weight="bernoulli", z=1e-4),
+    4: dict(N=8192, K=4096, V=128256, D=128, bias=True, weight=None, z=0.0),
+    5: dict(N=32768, K=4096, V=256000, D=256, bias=True, weight="ragged", z=1e-4, lead=(8, 4096)),
+}
+
+
+def make_inputs(cfg, device, seed=0):
+    """Draw order h, W, bias, E, target, weight; fp32 draws cast to bf16."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    N, K, V, D = cfg["N"], cfg["K"], cfg["V"], cfg["D"]
+    shape = (*cfg.get("lead", (N,)), K)
+    r = lambda *s, sc=1.0: sc * torch.randn(*s, device=device, generator=g)
+    h = r(*shape).to(torch.bfloat16)
+    W = r(V, K, sc=K ** -0.5).to(torch.bfloat16)
+    b = r(V, sc=0.02).to(torch.bfloat16) if cfg["bias"] else None
+    E = r(V, D).to(torch.bfloat16)
+    target = r(*shape[:-1], D)
+    weight = None
+    if cfg["weight"] == "bernoulli":
+        weight = (torch.rand(*shape[:-1], device=device, generator=g) >= 0.1).float()
+    elif cfg["weight"] == "ragged":
+        rows, T = shape[0], shape[1]
+        tails = torch.randint(0, 1025, (rows,), device=device, generator=g)
+        pos = torch.arange(T, device=device)[None, :]
+        weight = (pos < (T - tails)[:, None]).float()
+    params = [x.requires_grad_(True) for x in (h, W, E, b) if x is not None]
+    return h, W, E, b, target, weight, params
+
+
+def step_fn(swvr, h, W, E, b, target, weight, z, chunk):
+    return swvr.softmax_readout_mse(h, W, E, target, b, weight=weight, z_loss_weight=z, chunk_size=chunk)
+
+
+def algorithmic_flops(N, K, V, D):
+    fwd = 2.0 * N * V * (K + D)
+    return fwd, 2.0 * N * V * (4 * K + 3 * D)
+
+
+def kernel_flops(name, N, K, V, D):
+    """Algorithmic FLOPs of all launches of one kernel kind over one step."""
+    if name == "fwd_tile_kernel":
+        return 2.0 * N * V * (K + D)             # S = h W^T, P E
+    if name == "bwd_scores_kernel":
+        return 2.0 * N * V * (K + 2 * D)         # S recompute, dP = gO E^T, dE = P^T gO
+    if name == "bwd_gemm_kernel":
+        return 4.0 * N * V * K                   # dh = dS W, dW = dS^T h
+    return 0.0
+
+
+def cpu_baseline(cfg, tokens, chunk, device):
+    """Time oracle/chunked.py (the reference's CPU algorithm) fwd+bwd on `tokens` tokens."""
+    from oracle import chunked
+    N, K, V, D = cfg["N"], cfg["K"], cfg["V"], cfg["D"]
+    g = torch.Generator(device=device).manual_seed(1)
+    r = lambda *s, sc=1.0: (sc * torch.randn(*s, device=device, generator=g)).to(torch.bfloat16).cpu()
+    h, W, E = r(tokens, K), r(V, K, sc=K ** -0.5), r(V, D)
+    b = r(V, sc=0.02) if cfg["bias"] else None
+    gO = torch.randn(tokens, D) * 1e-3
+    glse = torch.randn(tokens) * 1e-4
+    threads = torch.get_num_threads()
+    t0 = time.perf_counter()
+    O, lse = chunked.forward(h, W, E, b, 1.0, chunk, torch.bfloat16)
+    chunked.backward(gO, glse, h, W, E, b, O, lse, 1.0, chunk, torch.bfloat16)
+    dt = time.perf_counter() - t0
+    _, flops = algorithmic_flops(tokens, K, V, D)
+    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"fwd+bwd of {tokens} tokens x the full V={V}, K={K}, D={D} (bf16 operands upcast "
+                      f"to fp32 BLAS, vocabulary chunk {chunk}) in {dt:.1f} s on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--chunk", type=int, default=8192)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=512)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only (N=1); multi-GPU runs are not part of it"}))
+        sys.exit(2)
+
+    import swvr_amd as swvr
+    from swvr_amd import _lib
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    N, K, V, D = cfg["N"], cfg["K"], cfg["V"], cfg["D"]
+    h, W, E, b, target, weight, params = make_inputs(cfg, dev)
+    run = lambda: step_fn(swvr, h, W, E, b, target, weight, cfg["z"], args.chunk)
+
+    def zero():
+        for p in params:
+            p.grad = None
+
+    # warm-up and peak memory above the inputs, grad buffers included (bench/bench.py:32-38)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    for _ in range(max(args.warmup, 1)):
+        zero()
+        run().backward()
+    torch.cuda.synchronize()
+    peak_gib = (torch.cuda.max_memory_allocated() - base) / 2**30
+
+    # forward only
+    fwd_iters = 5
+    with torch.no_grad():
+        run()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s0.record()
+        for _ in range(fwd_iters):
+            run()
+        s1.record()
+        torch.cuda.synchronize()
+    fwd_ms = s0.elapsed_time(s1) / fwd_iters
+
+    # timed fwd+bwd steps, every kernel launch bracketed by HIP events
+    _lib.kernel_timing(True)
+    _lib.kernel_timing(None)  # clear
+    zero()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        zero()
+        run().backward()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    kernels = _lib.kernel_timing(None)
+    _lib.kernel_timing(False)
+
+    fwd_flops, flops = algorithmic_flops(N, K, V, D)
+    tflops = flops / (ms * 1e-3) / 1e12
+    per_kernel = {}
+    for name, (kms, cnt) in kernels.items():
+        kf = kernel_flops(name, N, K, V, D) * args.steps
+        per_kernel[name] = {"ms_per_step": round(kms / args.steps, 3), "launches_per_step": cnt // args.steps,
+                            "avg_launch_ms": round(kms / cnt, 4),
+                            "tflops": round(kf / (kms * 1e-3) / 1e12, 1) if kf else None}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
+    dk = per_kernel[dom]
+    launch_flops = kernel_flops(dom, N, K, V, D) * args.steps / (dk["launches_per_step"] * args.steps)
+    achieved = launch_flops / (dk["avg_launch_ms"] * 1e-3) / 1e12
+    # W and E bytes the algorithm streams per step: fwd (W, E), bwd scores (W, E), dh GEMM (W)
+    we_bytes = (3 * V * K + 2 * V * D) * 2
+
+    out = {
+        "metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: fwd+bwd of softmax_readout_mse, N={N} K={K} V={V} D={D} bf16"
+                               + (", bias" if cfg["bias"] else "") + (f", weight {cfg['weight']}" if cfg["weight"] else "")
+                               + (f", z_loss {cfg['z']}" if cfg["z"] else ""),
+                   "N": N, "K": K, "V": V, "D": D, "chunk": args.chunk},
+        "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
+        "peak_gib": round(peak_gib, 3),
+        "we_stream_gbps": round(we_bytes / (ms * 1e-3) / 1e9, 1),
+        "kernels": per_kernel,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "published_reference_ms": {"A100": {3: 240, 2: 115, 4: 160}.get(args.config),
+                                   "H200": {3: 98, 2: 48, 4: 62}.get(args.config)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens, args.chunk, dev)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -50,9 +50,9 @@ hipEvent_t take_event() {
   return e;
 }
 
-const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",  "fwd_combine_kernel", "bwd_delta_kernel",
+const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
-                                     "fill_zero_kernel"};
+                                     "fill_zero_kernel",  "pack_vocab_kernel"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 
@@ -144,12 +144,7 @@ int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* 
   p.K = (int)K;
   p.V = (int)V;
   p.D = (int)D;
-  char* ws = static_cast<char*>(workspace);
-  const size_t per = (size_t)N * sizeof(float);
-  p.part_m = reinterpret_cast<float*>(ws);
-  p.part_l = reinterpret_cast<float*>(ws + plan.n_part * per);
-  p.part_acc = reinterpret_cast<float*>(ws + 2 * plan.n_part * per);
-  hipError_t e = fwd_launch(dtype, plan, p, O, lse, static_cast<hipStream_t>(stream));
+  hipError_t e = fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "forward launch");
   return SWVR_OK;
 }

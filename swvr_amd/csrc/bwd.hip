@@ -18,8 +18,6 @@ namespace swvr {
 
 namespace {
 
-constexpr int kBK = 32;
-
 __device__ __forceinline__ void store_as(void* base, int64_t idx, int dtype, float v) {
   if (dtype == kBF16)
     static_cast<bf16_t*>(base)[idx] = (bf16_t)v;
@@ -29,15 +27,29 @@ __device__ __forceinline__ void store_as(void* base, int64_t idx, int dtype, flo
     static_cast<float*>(base)[idx] = v;
 }
 
-// ---------------------------------------------------------------- delta
-__global__ __launch_bounds__(256) void bwd_delta_kernel(const float* __restrict__ O, const float* __restrict__ gO,
-                                                        const float* __restrict__ glse, int N, int D,
-                                                        float* __restrict__ delta) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  float s = 0.f;
-  for (int d = 0; d < D; ++d) s += O[(int64_t)n * D + d] * gO[(int64_t)n * D + d];
-  delta[n] = s - glse[n];
+// ---------------------------------------------------------------- token-side packing
+// delta = rowsum(O * gO) - gLSE (swvr/chunked.py:113-114), and the token-side
+// operands of the scores kernel packed over N_pad rows: gO rounded to the
+// compute dtype (swvr/chunked.py:115) as [N_pad][DP] (zero padded), and
+// [lse | delta] as 2 x N_pad floats (lse = +inf on padding rows: P = 0 there).
+template <class T>
+__global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__ O, const float* __restrict__ gO,
+                                                       const float* __restrict__ lse,
+                                                       const float* __restrict__ glse, int N, int D, int N_pad,
+                                                       int DP, T* __restrict__ gOp, float* __restrict__ lsed) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N_pad * DP) return;
+  const int n = (int)(e / DP), d = (int)(e % DP);
+  gOp[e] = (n < N && d < D) ? from_float<T>(gO[(int64_t)n * D + d]) : (T)0.f;
+  if (d == 0) {
+    float s = 0.f;
+    if (n < N) {
+      for (int k = 0; k < D; ++k) s += O[(int64_t)n * D + k] * gO[(int64_t)n * D + k];
+      s -= glse[n];
+    }
+    lsed[n] = n < N ? lse[n] : kPosInf;
+    lsed[N_pad + n] = s;
+  }
 }
 
 // ---------------------------------------------------------------- scores
@@ -46,84 +58,21 @@ struct ScoresParams {
   int64_t ldh;
   const void* W;
   int64_t ldw;
-  const void* E;
-  int64_t lde;
-  const float* bias;
+  const void* Ep;       // packed E [V_pad][DP]
+  const float* biasp;   // packed bias [V_pad]
   float scale;
-  int N, K, D;
-  const float* lse;
-  const float* delta;
-  const float* gO;  // fp32 [N][D]
-  int v0, cv;       // chunk start and rows
-  int C;            // chunk stride of the partials (multiple of BV)
+  int N, K;
+  const void* gOp;      // packed gO [N_pad][DP]
+  const float* lsed;    // [lse | delta], 2 x N_pad
+  int N_pad;
+  int v0, cv;           // chunk start and rows
+  int C;                // chunk stride of the partials (multiple of BV)
   int n_tb, G, n_vtc;
-  void* stage;      // [C][ld_stage] compute dtype, token index contiguous
+  void* stage;          // [C][ld_stage] compute dtype, token index contiguous
   int64_t ld_stage;
-  float* part_dE;   // [G][DP][C]
-  float* part_db;   // [G][C]
+  float* part_dE;       // [G][DP][C]
+  float* part_db;       // [G][C]
   int need_stage, need_dE, need_db;
-};
-
-// gO tile (rounded to the compute dtype, as swvr/chunked.py:115 rounds it),
-// LSE and delta of one token block, loaded during the first stages of the
-// block's reduction loop.
-template <class T, int BM, int DP, int DPE>
-struct ScoresSide {
-  static constexpr int PER = 8;
-  static constexpr int TOTAL = BM * DP;
-  static constexpr int BATCH = kThreads * PER;
-  static constexpr int ITERS = (TOTAL + BATCH - 1) / BATCH;
-  T* sG;
-  float* sLse;
-  float* sDelta;
-  const float* gO;
-  const float* lse;
-  const float* delta;
-  int n0, N, D;
-  float gv[PER];
-  float lv, dv;
-
-  __device__ __forceinline__ void load(int it) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = (it * PER + q) * kThreads + (int)threadIdx.x;
-      const int tl = e / DP, d = e % DP;
-      const bool ok = e < TOTAL && n0 + tl < N && d < D;
-      gv[q] = ok ? gO[(int64_t)(n0 + tl) * D + d] : 0.f;
-    }
-    if (it == 0 && (int)threadIdx.x < BM) {
-      const int n = n0 + (int)threadIdx.x;
-      // padding tokens: P = exp(x - inf) = 0
-      lv = n < N ? lse[n] : kPosInf;
-      dv = n < N ? delta[n] : 0.f;
-    }
-  }
-  __device__ __forceinline__ void store(int it) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = (it * PER + q) * kThreads + (int)threadIdx.x;
-      if (e < TOTAL) sG[(e / DP) * DPE + e % DP] = from_float<T>(gv[q]);
-    }
-    if (it == 0 && (int)threadIdx.x < BM) {
-      sLse[threadIdx.x] = lv;
-      sDelta[threadIdx.x] = dv;
-    }
-  }
-  __device__ __forceinline__ void pre(int kt) {
-    if (kt < ITERS) load(kt);
-  }
-  __device__ __forceinline__ void post(int kt) {
-    if (kt < ITERS) store(kt);
-  }
-  __device__ __forceinline__ void finish(int nk) {
-    if (nk < ITERS) {
-      for (int it = nk; it < ITERS; ++it) {
-        load(it);
-        store(it);
-      }
-      __syncthreads();
-    }
-  }
 };
 
 // One workgroup: BV vocabulary rows of the chunk x one group of token
@@ -135,19 +84,23 @@ struct ScoresSide {
 template <class T, int BM, int BV, int DP>
 __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
   typedef typename Vec8<T>::type V8;
-  constexpr int LDR = LdsRow<T, kBK>::value;
-  constexpr int DPE = DP + 16 / (int)sizeof(T);
+  constexpr int kBK = SliceK<T>::value;
+  typedef KTile<T, BM, kBK> TA;  // h rows of the token block
+  typedef KTile<T, BV, kBK> TB;  // W rows of the vocabulary tile
+  typedef KTile<T, BV, DP> TE;   // E tile
+  typedef KTile<T, BM, DP> TG;   // gO tile
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;
   constexpr int FT = BM / 32, FV = BV / 128;
   constexpr int DB = DP / 32, DK = DP / 16;
   constexpr int WVR = BV / 4;  // vocabulary rows per wave
 
-  __shared__ __attribute__((aligned(16))) T sH[2][BM * LDR];
-  __shared__ __attribute__((aligned(16))) T sW[2][BV * LDR];
-  __shared__ __attribute__((aligned(16))) T sE[BV * DPE];
-  __shared__ __attribute__((aligned(16))) T sG[BM * DPE];
-  __shared__ float sBias[BV];
-  __shared__ float sLse[BM];
-  __shared__ float sDelta[BM];
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB + TE::BYTES + TG::BYTES + BV * 4 + 2 * BM * 4];
+  char* const sE = smem + kStages * SB;
+  char* const sG = sE + TE::BYTES;
+  float* const sBias = reinterpret_cast<float*>(sG + TG::BYTES);
+  float* const sLse = sBias + BV;
+  float* const sDelta = sLse + BM;
 
   const int lane = lane_id(), w = wave_id();
   const int t = xcd_swizzle(blockIdx.x, p.n_vtc * p.G);
@@ -157,15 +110,14 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
   const int rows = p.cv - vl0;  // valid rows of this tile (may exceed BV)
   const int tb_begin = (int)((int64_t)g * p.n_tb / p.G);
   const int tb_end = (int)((int64_t)(g + 1) * p.n_tb / p.G);
-  const T* E = static_cast<const T*>(p.E);
 
-  for (int e = threadIdx.x; e < BV * DP; e += kThreads) {
-    const int vv = e / DP, d = e % DP;
-    sE[vv * DPE + d] = (vv < rows && d < p.D) ? E[(int64_t)(vg0 + vv) * p.lde + d] : (T)0.f;
-  }
-  if ((int)threadIdx.x < BV) {
-    const int vv = threadIdx.x;
-    sBias[vv] = vv < rows ? (p.bias ? p.bias[vg0 + vv] : 0.f) : kNegInf;
+  // E and bias of the vocabulary tile: once per workgroup, ahead of the stages
+  {
+    TE te;
+    te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP);
+    te.issue(sE, 0);
+    if ((int)threadIdx.x * 16 < BV * 4)
+      dma16(make_rsrc(p.biasp + vg0), (uint32_t)threadIdx.x * 16, (char*)sBias + w * 1024);
   }
 
   f32x16_t deacc[DB][FV];
@@ -177,54 +129,75 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
     for (int db = 0; db < DB; ++db) deacc[db][fv] = zero16();
   }
 
-  KTile<T, BM, kBK> th;
-  th.ld = p.ldh;
-  th.k_valid = p.K;
-  KTile<T, BV, kBK> tw;
-  tw.base = static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw;
-  tw.ld = p.ldw;
-  tw.rows_valid = rows;
-  tw.k_valid = p.K;
   const int nk = (p.K + kBK - 1) / kBK;
+  const int total = (tb_end - tb_begin) * nk;
+  const T* h = static_cast<const T*>(p.h);
+  TA ta;
+  ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
+  TB tw;
+  tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
+  auto issue = [&](int gs) {
+    const int kt = gs % nk;
+    if (kt == 0) {
+      const int n0 = (tb_begin + gs / nk) * BM;
+      ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
+    }
+    char* st = smem + (gs % kStages) * SB;
+    ta.issue(st, kt * kBK);
+    tw.issue(st + TA::BYTES, kt * kBK);
+  };
+#pragma unroll
+  for (int gs = 0; gs < kStages - 1; ++gs)
+    if (gs < total) issue(gs);
+
   T* stage = static_cast<T*>(p.stage);
-
-  for (int tb = tb_begin; tb < tb_end; ++tb) {
-    const int n0 = tb * BM;
-    th.base = static_cast<const T*>(p.h) + (int64_t)n0 * p.ldh;
-    th.rows_valid = p.N - n0;
-    ScoresSide<T, BM, DP, DPE> side;
-    side.sG = sG;
-    side.sLse = sLse;
-    side.sDelta = sDelta;
-    side.gO = p.gO;
-    side.lse = p.lse;
-    side.delta = p.delta;
-    side.n0 = n0;
-    side.N = p.N;
-    side.D = p.D;
-
-    f32x16_t sacc[FT][FV];
+  f32x16_t sacc[FT][FV];
+  for (int gs = 0; gs < total; ++gs) {
+    const int kt = gs % nk;
+    const int n0 = (tb_begin + gs / nk) * BM;
+    const int ahead = total - 1 - gs < kStages - 2 ? total - 1 - gs : kStages - 2;
+    wait_stages<L, kStages>(ahead);
+    stage_barrier();
+    if (gs + kStages - 1 < total) issue(gs + kStages - 1);
+    if (kt == 0) {
+      // gO, LSE and delta of this token block; every wave has finished the
+      // previous block's epilogue (barrier above)
+      TG tg;
+      tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
+      tg.issue(sG, 0);
+      const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
+      if (c < BM / 2) {
+        const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
+        dma16(make_rsrc(p.lsed), off, (char*)sLse + w * 1024);
+      }
 #pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
+      for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
-      for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
-    reduce_loop<T, kBK, FT, FV>(sacc, th, tw, sH[0], sH[1], sW[0], sW[1], p.K, 0, w * WVR, side);
-    side.finish(nk);
+        for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+    }
+    const char* st = smem + (gs % kStages) * SB;
+    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, 0, w * WVR);
+    if (kt != nk - 1) continue;
+    if (nk < kStages || gs < kStages) {
+      // short reduction, or the first block (E / bias were issued before the
+      // stages): make sure every side load has landed
+      wait_vmcnt<0>();
+      stage_barrier();
+    }
 
+    TG tgl;  // layout only
+    TE tel;
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv) {
       const int vl = w * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
-      const float bvv = sBias[vl];
+      const float bvv = vl < rows ? sBias[vl] : kNegInf;
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
         // dP block = gO[tokens] E[rows]^T over D
         f32x16_t dp = zero16();
 #pragma unroll
-        for (int kd = 0; kd < DK; ++kd) {
-          const V8 a = *reinterpret_cast<const V8*>(sG + (ft * 32 + (lane & 31)) * DPE + kd * 16 + (lane >> 5) * 8);
-          const V8 b = *reinterpret_cast<const V8*>(sE + vl * DPE + kd * 16 + (lane >> 5) * 8);
-          mfma_k16(dp, a, b);
-        }
+        for (int kd = 0; kd < DK; ++kd)
+          mfma_k16(dp, read_op(tgl, sG, ft * 32 + (lane & 31), kd), read_op(tel, sE, vl, kd));
         float dbs = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -268,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
 #pragma unroll
               for (int tt = 0; tt < 8; ++tt) {
                 const int tl = ft * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-                av[tt] = sG[tl * DPE + db * 32 + (lane & 31)];
+                av[tt] = *reinterpret_cast<const T*>(sG + TG::elem(tl, db * 32 + (lane & 31)));
               }
               mfma_k16(deacc[db][fv], av, bv);
             }
@@ -318,103 +291,141 @@ struct GemmParams {
   int dh_first, dh_last;
 };
 
-// One launch covers both gradient products of a chunk:
-//   blocks [0, n_dw):          dW[v0+v][k]  = sum_tok stage[v][tok] h[tok][k]
-//   blocks [n_dw, n_dw+n_dh):  dh[tok][k] += sum_v  stage[v][tok] W[v0+v][k]
-// The dW tiles (the longer reduction) are dealt first.
-template <class T, int GM, int GN>
-__global__ __launch_bounds__(kThreads) void bwd_gemm_kernel(GemmParams p) {
-  constexpr int FM = GM / 64, FN = GN / 64;
-  constexpr int LDR = LdsRow<T, kBK>::value;
-  __shared__ __attribute__((aligned(16))) T sA[2][GM * LDR];
-  __shared__ __attribute__((aligned(16))) T sB[2][GN * LDR];
+// Write a GEMM accumulator tile: out[(row_off + row) * ld + col] = acc (+ prev[...]),
+// rows < rows, cols < ld.  prev (fp32, may alias out) is added when non-null.
+template <int FM, int FN, class OutT>
+__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], OutT* out, const float* prev,
+                                           int64_t row_off, int rows, int row0, int col0, int ld) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int col = col0 + fn * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + fm * 32 + c_row(r, lane);
+        if (row < rows && col < ld) {
+          const int64_t idx = (row_off + row) * ld + col;
+          float v = acc[fm][fn][r];
+          if (prev) v += prev[idx];
+          out[idx] = (OutT)v;
+        }
+      }
+    }
+}
 
-  const int lane = lane_id(), w = wave_id();
+// Single-tile pipelined reduction: acc += A[.., 0:k_total] B[.., 0:k_total]^T.
+template <class T, int BK, int FM, int FN, class TA, class TB>
+__device__ __forceinline__ void gemm_loop(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, char* smem,
+                                          int k_total, int a_row0, int b_row0) {
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;
+  const int nk = (k_total + BK - 1) / BK;
+#pragma unroll
+  for (int gs = 0; gs < kStages - 1; ++gs)
+    if (gs < nk) {
+      ta.issue(smem + gs * SB, gs * BK);
+      tb.issue(smem + gs * SB + TA::BYTES, gs * BK);
+    }
+  for (int gs = 0; gs < nk; ++gs) {
+    const int ahead = nk - 1 - gs < kStages - 2 ? nk - 1 - gs : kStages - 2;
+    wait_stages<L, kStages>(ahead);
+    stage_barrier();
+    if (gs + kStages - 1 < nk) {
+      char* st = smem + ((gs + kStages - 1) % kStages) * SB;
+      ta.issue(st, (gs + kStages - 1) * BK);
+      tb.issue(st + TA::BYTES, (gs + kStages - 1) * BK);
+    }
+    const char* st = smem + (gs % kStages) * SB;
+    stage_mma<T, BK, FM, FN>(acc, ta, tb, st, st + TA::BYTES, a_row0, b_row0);
+  }
+}
+
+// One tile of one gradient product; DW selects the product:
+//   DW:  dW[v0+v][k]  = sum_tok stage[v][tok] h[tok][k]     (A: KTile, B: RTile)
+//   !DW: dh[tok][k]  += sum_v  stage[v][tok] W[v0+v][k]      (A: RTile, B: RTile)
+template <class T, int GM, int GN, bool DW>
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem) {
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int FM = GM / 64, FN = GN / 64;
+  const int w = wave_id();
   const int wm = w >> 1, wn = w & 1;
+  const int mt = t / p.n_n, nt = t % p.n_n;
   const T* stage = static_cast<const T*>(p.stage);
   f32x16_t acc[FM][FN];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = zero16();
-  NoSide none;
-  const int b = blockIdx.x;
-  if (b < p.n_dw) {
-    const int t = xcd_swizzle(b, p.n_dw);
-    const int mt = t / p.n_n, nt = t % p.n_n;
+  RTile<T, GN, kBK> tb;
+  if constexpr (DW) {
     KTile<T, GM, kBK> ta;
-    ta.base = stage + (int64_t)mt * GM * p.ld_stage;
-    ta.ld = p.ld_stage;
-    ta.rows_valid = p.cv - mt * GM;
-    ta.k_valid = (int)p.N_pad;
-    RTile<T, GN, kBK> tb;
-    tb.base = static_cast<const T*>(p.h) + nt * GN;
-    tb.ld = p.ldh;
-    tb.rows_valid = p.K - nt * GN;
-    tb.k_valid = p.N;
-    reduce_loop<T, kBK, FM, FN>(acc, ta, tb, sA[0], sA[1], sB[0], sB[1], p.N, wm * (GM / 2), wn * (GN / 2), none);
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int col = nt * GN + wn * (GN / 2) + fn * 32 + (lane & 31);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = mt * GM + wm * (GM / 2) + fm * 32 + c_row(r, lane);
-          if (row < p.cv && col < p.K) store_as(p.gW, (int64_t)(p.v0 + row) * p.K + col, p.gW_dtype, acc[fm][fn][r]);
-        }
-      }
+    ta.setup(stage + (int64_t)mt * GM * p.ld_stage, p.ld_stage, p.cv - mt * GM, p.N);
+    tb.setup(static_cast<const T*>(p.h) + nt * GN, p.ldh, p.K - nt * GN, p.N);
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.N, wm * (GM / 2), wn * (GN / 2));
   } else {
-    const int t = xcd_swizzle(b - p.n_dw, p.n_dh);
-    const int mt = t / p.n_n, nt = t % p.n_n;
     RTile<T, GM, kBK> ta;
-    ta.base = stage + (int64_t)mt * GM;
-    ta.ld = p.ld_stage;
-    ta.rows_valid = (int)(p.N_pad - (int64_t)mt * GM);
-    ta.k_valid = p.cv;
-    RTile<T, GN, kBK> tb;
-    tb.base = static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN;
-    tb.ld = p.ldw;
-    tb.rows_valid = p.K - nt * GN;
-    tb.k_valid = p.cv;
-    reduce_loop<T, kBK, FM, FN>(acc, ta, tb, sA[0], sA[1], sB[0], sB[1], p.cv, wm * (GM / 2), wn * (GN / 2), none);
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int col = nt * GN + wn * (GN / 2) + fn * 32 + (lane & 31);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = mt * GM + wm * (GM / 2) + fm * 32 + c_row(r, lane);
-          if (row < p.N && col < p.K) {
-            const int64_t idx = (int64_t)row * p.K + col;
-            float v = acc[fm][fn][r];
-            if (!p.dh_first) v += p.dh_acc[idx];
-            if (p.dh_last)
-              store_as(p.gh, idx, p.gh_dtype, v);
-            else
-              p.dh_acc[idx] = v;
-          }
-        }
-      }
+    ta.setup(stage + (int64_t)mt * GM, p.ld_stage, (int)(p.N_pad - (int64_t)mt * GM), p.cv);
+    tb.setup(static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / 2), wn * (GN / 2));
+  }
+  const int rows = DW ? p.cv : p.N;
+  const int row0 = mt * GM + wm * (GM / 2);
+  const int col0 = nt * GN + wn * (GN / 2);
+  // dispatch on the output dtype outside the unrolled store loops
+  if constexpr (DW) {
+    if (p.gW_dtype == kBF16)
+      gemm_store<FM, FN>(acc, static_cast<bf16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+    else if (p.gW_dtype == kF16)
+      gemm_store<FM, FN>(acc, static_cast<f16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+    else
+      gemm_store<FM, FN>(acc, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+  } else {
+    const float* prev = p.dh_first ? nullptr : p.dh_acc;
+    if (!p.dh_last)
+      gemm_store<FM, FN>(acc, p.dh_acc, prev, 0, rows, row0, col0, p.K);
+    else if (p.gh_dtype == kBF16)
+      gemm_store<FM, FN>(acc, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+    else if (p.gh_dtype == kF16)
+      gemm_store<FM, FN>(acc, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+    else
+      gemm_store<FM, FN>(acc, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
   }
 }
 
+// One launch covers both gradient products of a chunk: blocks [0, n_dw) are
+// dW tiles, blocks [n_dw, n_dw + n_dh) dh tiles.  The dW tiles (the longer
+// reduction, over all tokens) are dealt first.
+template <class T, int GM, int GN>
+__global__ __launch_bounds__(kThreads) void bwd_gemm_kernel(GemmParams p) {
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int SB = KTile<T, GM, kBK>::BYTES + RTile<T, GN, kBK>::BYTES;
+  static_assert(KTile<T, GM, kBK>::BYTES == RTile<T, GM, kBK>::BYTES, "both A layouts stage the same bytes");
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB];
+  const int b = blockIdx.x;
+  if (b < p.n_dw)
+    gemm_tile<T, GM, GN, true>(p, xcd_swizzle(b, p.n_dw), smem);
+  else
+    gemm_tile<T, GM, GN, false>(p, xcd_swizzle(b - p.n_dw, p.n_dh), smem);
+}
+
 // ---------------------------------------------------------------- dE / db
+// One thread per (row, d) of gE plus one per row of gb; consecutive threads
+// take consecutive rows, so the partial reads are coalesced.
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict__ part_dE,
                                                          const float* __restrict__ part_db, int G, int C, int DP,
                                                          int v0, int cv, int D, void* gE, int gE_dtype,
                                                          float* gb) {
-  const int v = blockIdx.x * blockDim.x + threadIdx.x;
-  if (v >= cv) return;
-  if (gE) {
-    for (int d = 0; d < D; ++d) {
-      float s = 0.f;
-      for (int g = 0; g < G; ++g) s += part_dE[((int64_t)g * DP + d) * C + v];
-      store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, s);
-    }
-  }
-  if (gb) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n_e = gE ? (int64_t)cv * D : 0;
+  if (e < n_e) {
+    const int d = (int)(e / cv), v = (int)(e % cv);
+    float s = 0.f;
+    for (int g = 0; g < G; ++g) s += part_dE[((int64_t)g * DP + d) * C + v];
+    store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, s);
+  } else if (gb && e < n_e + cv) {
+    const int v = (int)(e - n_e);
     float s = 0.f;
     for (int g = 0; g < G; ++g) s += part_db[(int64_t)g * C + v];
     gb[v0 + v] = s;
@@ -448,8 +459,8 @@ hipError_t launch_scores(const ScoresParams& sp, hipStream_t stream) {
 }
 
 // Tile shape of the scores kernel per (dtype, padded D): dE^T (DP x BV/4 per
-// wave) and the score block (BM x BV/4 per wave) share the register file; E,
-// the gO tile and two K-slices of h and W share LDS.
+// wave) and the score block (BM x BV/4 per wave) share the register file; the
+// stage ring, E, and the gO tile share LDS.
 template <class T, int DP>
 struct ScoresTile {
   static constexpr bool wide = sizeof(T) == 2;
@@ -498,16 +509,29 @@ template <class T>
 hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) {
   hipError_t e;
   char* ws = p.ws;
-  float* delta = reinterpret_cast<float*>(ws + plan.off_delta);
   T* stage = reinterpret_cast<T*>(ws + plan.off_stage);
   float* part_dE = reinterpret_cast<float*>(ws + plan.off_pe);
   float* part_db = reinterpret_cast<float*>(ws + plan.off_pb);
   float* dh_acc = plan.dh_acc ? reinterpret_cast<float*>(ws + plan.off_dh) : nullptr;
+  T* gOp = reinterpret_cast<T*>(ws + plan.off_gO);
+  float* lsed = reinterpret_cast<float*>(ws + plan.off_lsed);
+  T* Ep = reinterpret_cast<T*>(ws + plan.off_Ep);
+  float* biasp = reinterpret_cast<float*>(ws + plan.off_bias);
 
-  timing_begin(kKindBwdDelta, stream);
-  bwd_delta_kernel<<<(p.N + 255) / 256, 256, 0, stream>>>(p.O, p.gO, p.glse, p.N, p.D, delta);
-  timing_end(kKindBwdDelta, stream);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  {
+    const int64_t n = (int64_t)plan.N_pad * plan.DP;
+    timing_begin(kKindBwdDelta, stream);
+    bwd_pack_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(p.O, p.gO, p.lse, p.glse, p.N, p.D,
+                                                                   (int)plan.N_pad, plan.DP, gOp, lsed);
+    timing_end(kKindBwdDelta, stream);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const int64_t nv = (int64_t)plan.V_pad * plan.DP;
+    timing_begin(kKindPack, stream);
+    pack_vocab_kernel<T><<<(int)((nv + 255) / 256), 256, 0, stream>>>(
+        static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp);
+    timing_end(kKindPack, stream);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
 
   const bool need_stage = p.gh || p.gW;
   for (int c = 0; c < plan.n_chunks; ++c) {
@@ -518,16 +542,14 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.ldh = p.ldh;
     sp.W = p.W;
     sp.ldw = p.ldw;
-    sp.E = p.E;
-    sp.lde = p.lde;
-    sp.bias = p.bias;
+    sp.Ep = Ep;
+    sp.biasp = biasp;
     sp.scale = p.scale;
     sp.N = p.N;
     sp.K = p.K;
-    sp.D = p.D;
-    sp.lse = p.lse;
-    sp.delta = delta;
-    sp.gO = p.gO;
+    sp.gOp = gOp;
+    sp.lsed = lsed;
+    sp.N_pad = (int)plan.N_pad;
     sp.v0 = v0;
     sp.cv = cv;
     sp.C = (int)plan.C;
@@ -570,8 +592,10 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     }
     if (p.gE || p.gb) {
       timing_begin(kKindBwdReduce, stream);
-      bwd_reduce_kernel<<<(cv + 255) / 256, 256, 0, stream>>>(part_dE, part_db, plan.G, (int)plan.C, plan.DP, v0, cv,
-                                                              p.D, p.gE, p.gE_dtype, p.gb);
+      const int64_t n_threads = (p.gE ? (int64_t)cv * p.D : 0) + (p.gb ? cv : 0);
+      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(part_dE, part_db, plan.G, (int)plan.C,
+                                                                            plan.DP, v0, cv, p.D, p.gE, p.gE_dtype,
+                                                                            p.gb);
       timing_end(kKindBwdReduce, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
@@ -630,17 +654,25 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G < 1) G = 1;
   plan->G = G;
   plan->dh_acc = need_gh && plan->n_chunks > 1;
+  plan->V_pad = ((V + BV - 1) / BV) * BV;
+  const size_t tb = dtype_bytes(dtype);
   size_t off = 0;
-  plan->off_delta = off;
-  off += align256((size_t)N * 4);
   plan->off_stage = off;
-  off += align256((size_t)c * (size_t)plan->N_pad * dtype_bytes(dtype));
+  off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pe = off;
   off += align256((size_t)G * DP * c * 4);
   plan->off_pb = off;
   off += align256((size_t)G * c * 4);
   plan->off_dh = off;
   if (plan->dh_acc) off += align256((size_t)N * K * 4);
+  plan->off_gO = off;
+  off += align256((size_t)plan->N_pad * DP * tb);
+  plan->off_lsed = off;
+  off += align256((size_t)plan->N_pad * 2 * 4);
+  plan->off_Ep = off;
+  off += align256((size_t)plan->V_pad * DP * tb);
+  plan->off_bias = off;
+  off += align256((size_t)plan->V_pad * 4);
   plan->ws_bytes = off;
   return true;
 }

@@ -72,193 +72,292 @@ template <class T> __device__ __forceinline__ float to_float(T x) { return (floa
 // Row of the C/D block held by register r of this lane.
 __device__ __forceinline__ int c_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
-// Stride (elements) of one operand row in LDS: BK plus 16 bytes of padding,
-// which spreads the 32 rows a ds_read_b128 touches over all banks.
-template <class T, int BK> struct LdsRow { static constexpr int value = BK + 16 / (int)sizeof(T); };
+// ----------------------------------------------------------------------------
+// Direct-to-LDS operand pipeline.
+//
+// Operand tiles move HBM -> LDS with buffer_load_dwordx4 ... lds: each lane
+// names a 16-byte source chunk, the wave's 64 chunks land contiguously in LDS,
+// and no registers are used, so the reduction loop keeps kStages-1 slices in
+// flight.  A buffer resource whose range is 2^31-1 bytes turns any chunk the
+// tile does not own (rows or k beyond the operand) into a zero fill: such a
+// lane's offset is set to kOOB, past the range.
+//
+// LDS tile layouts (16-byte chunks, XOR-swizzled within a row so that the
+// MFMA operand reads are free of bank conflicts):
+//   KTile: [R rows][BK] elements, the reduction index contiguous in global
+//          memory (element (r, k) at base[r * ld + k]); operand read = one
+//          ds_read_b128 (bf16/f16) or two (f32) per lane.
+//   RTile: [BK][R] elements, the row index contiguous in global memory
+//          (element (r, k) at base[k * ld + r]); operand read transposes in
+//          the LDS read: two ds_read_b64_tr_b16 per lane (bf16/f16), or eight
+//          ds_read_b32 (f32).
+// ----------------------------------------------------------------------------
+typedef int rsrc_t __attribute__((ext_vector_type(4)));  // buffer descriptor (4 SGPRs)
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-// ----------------------------------------------------------------------------
-// Operand tiles staged global -> registers -> LDS.  LDS always holds a tile as
-// [row][k] with k contiguous (stride LdsRow), which is what the MFMA operand
-// reads want.  Global memory may hold it either way:
-//   KTile: element (r, k) at base[r * ld + k]   (reduction index contiguous)
-//   RTile: element (r, k) at base[k * ld + r]   (row index contiguous); the
-//          tile is transposed in registers (8x8-byte blocks) on its way to LDS.
-// Rows >= rows_valid and k >= k_valid read as zero.  k_valid is a multiple of
-// 16 bytes worth of elements for KTile (the host checks K % 8 == 0) and rows of
-// an RTile come in groups of 8 bytes (row counts are multiples of 8).
-// ----------------------------------------------------------------------------
+constexpr int kStages = 4;   // LDS ring depth of the reduction loop
+constexpr uint32_t kOOB = 0x80000000u;
+
+// Reduction slice per stage: 32 elements (64-byte rows) for bf16 / f16, 16
+// (64-byte rows) for f32, which keeps the four-stage ring inside LDS.
+template <class T> struct SliceK { static constexpr int value = sizeof(T) == 2 ? 32 : 16; };
+
+// XOR swizzle of the 16-byte chunks of an LDS row of `cpr` chunks: the eight
+// rows that a ds_read_b128 serves in one pass land on distinct banks.
+__device__ __forceinline__ int chunk_swizzle(int row, int cpr) {
+  return cpr >= 8 ? (row & 7) : (row / (8 / cpr)) % cpr;
+}
+
+// Raw buffer descriptor over [base, base + 2^31 - 1): stride 0, 32-bit data
+// format (the CDNA descriptor's fourth dword); a null base gives an empty
+// range, so every load through it returns zeros.  base must be wave-uniform.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  rsrc_t r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xFFFFu));
+  r.z = base ? 0x7FFFFFFF : 0;
+  r.w = 0x00020000;
+  return r;
+}
+
+// One 16-byte chunk per lane into LDS at wave_base + 16 * lane
+// (buffer_load_dwordx4 ... lds; M0 holds the wave's LDS base).  Issued from
+// inline assembly so that the compiler does not guard every later LDS read
+// with a wait for all outstanding loads: the reduction loops order these
+// loads themselves (wait_stages + stage_barrier).  M0 is restored.
+__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, void* wave_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(size_t)(__attribute__((address_space(3))) char*)wave_base);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(voff), "s"(r), "s"(lds)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() carries a
+// release fence that waits for every outstanding vector memory operation
+// (vmcnt(0)), which would drain the whole prefetch ring; the stage data here
+// is already covered by the explicit vmcnt wait that precedes the barrier, so
+// only LDS traffic (lgkmcnt) is waited for.  The "memory" clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until at most `ahead` stages of L loads per thread are outstanding.
+template <int L, int NS>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  static_assert(NS == 4, "ring depth");
+  if (ahead >= 2)
+    wait_vmcnt<2 * L>();
+  else if (ahead == 1)
+    wait_vmcnt<L>();
+  else
+    wait_vmcnt<0>();
+}
+
 template <class T, int R, int BK>
 struct KTile {
-  static constexpr int CE = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-  static constexpr int CPR = BK / CE;             // chunks per row
-  static constexpr int TOTAL = R * CPR;
-  static constexpr int NCH = (TOTAL + kThreads - 1) / kThreads;
-  static constexpr int LDR = LdsRow<T, BK>::value;
-  uint4 v[NCH];
-  const T* base;
-  int64_t ld;
-  int rows_valid;
+  static constexpr int CE = 16 / (int)sizeof(T);    // elements per chunk
+  static constexpr int CPR = BK / CE;               // chunks per LDS row
+  static constexpr int ROWB = BK * (int)sizeof(T);  // bytes per LDS row
+  static constexpr int BYTES = R * ROWB;
+  static constexpr int NI = BYTES / (kThreads * 16);  // loads per thread per stage
+  static_assert(BYTES % (kThreads * 16) == 0, "tile must be a whole number of wave loads");
+  static_assert(CPR >= 4 && (CPR & (CPR - 1)) == 0, "rows of 4, 8, 16, ... chunks");
+
+  __device__ static __forceinline__ int swz(int row) { return chunk_swizzle(row, CPR); }
+  // Byte offset of element (row, col) in the staged tile.
+  __device__ static __forceinline__ int elem(int row, int col) {
+    return row * ROWB + (((col / CE) ^ swz(row)) * 16) + (col % CE) * (int)sizeof(T);
+  }
+
+  const char* base;  // element (0, 0)
+  int64_t ldb;       // row stride in bytes
+  uint32_t off[NI];  // byte offset of this lane's chunk at k = 0, or kOOB
+  int kc[NI];        // first reduction index of the chunk
   int k_valid;
 
-  __device__ __forceinline__ void load(int k0) {
+  __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv) {
+    base = reinterpret_cast<const char*>(b);
+    ldb = ld * (int64_t)sizeof(T);
+    k_valid = kv;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = i * kThreads + (int)threadIdx.x;
-      const int r = c / CPR, kc = (c % CPR) * CE;
-      const bool ok = (TOTAL % kThreads == 0 || c < TOTAL) && r < rows_valid && k0 + kc < k_valid;
-      v[i] = ok ? *reinterpret_cast<const uint4*>(base + (int64_t)r * ld + (k0 + kc)) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NI; ++i) {
+      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
+      const int row = lin / ROWB, slot = (lin % ROWB) / 16;
+      kc[i] = (slot ^ swz(row)) * CE;
+      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc[i] * (int)sizeof(T)) : kOOB;
     }
   }
-  __device__ __forceinline__ void store(T* lds) const {
+  // New rows, same shape (the per-lane offsets only depend on rows_valid).
+  __device__ __forceinline__ void rebase(const T* b, int rows_valid) {
+    base = reinterpret_cast<const char*>(b);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = i * kThreads + (int)threadIdx.x;
-      if (TOTAL % kThreads == 0 || c < TOTAL) {
-        const int r = c / CPR, kc = (c % CPR) * CE;
-        *reinterpret_cast<uint4*>(lds + r * LDR + kc) = v[i];
-      }
+    for (int i = 0; i < NI; ++i) {
+      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
+      const int row = lin / ROWB;
+      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc[i] * (int)sizeof(T)) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void issue(char* stage, int k0) const {
+    const rsrc_t r = make_rsrc(base + (int64_t)k0 * (int)sizeof(T));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const uint32_t v = (off[i] == kOOB || k0 + kc[i] >= k_valid) ? kOOB : off[i];
+      dma16(r, v, stage + (i * kThreads + wave_id() * 64) * 16);
     }
   }
 };
 
 template <class T, int R, int BK>
 struct RTile {
-  static constexpr int RB = 8 / (int)sizeof(T);  // rows per 8-byte block
-  static constexpr int NRB = R / RB;
-  static constexpr int TOTAL = (BK / 8) * NRB;   // 8(k) x RB(r) blocks
-  static constexpr int NB = (TOTAL + kThreads - 1) / kThreads;
-  static constexpr int LDR = LdsRow<T, BK>::value;
-  uint2 v[NB][8];
-  const T* base;
-  int64_t ld;
-  int rows_valid;
+  static constexpr int CE = 16 / (int)sizeof(T);
+  static constexpr int ROWB = R * (int)sizeof(T);  // bytes per LDS k-row
+  static constexpr int BYTES = BK * ROWB;
+  static constexpr int NI = BYTES / (kThreads * 16);
+  static_assert(BYTES % (kThreads * 16) == 0, "tile must be a whole number of wave loads");
+  static_assert(ROWB >= 128, "swizzle needs 8 chunks per k-row");
+
+  __device__ static __forceinline__ int swz(int krow) { return (krow & 3) * 2; }
+
+  const char* base;  // element (r = 0, k = 0)
+  int64_t ldb;       // k-row stride in bytes
+  uint32_t off[NI];
+  int kr[NI];        // k-row of the chunk within the stage
   int k_valid;
 
-  __device__ __forceinline__ void load(int k0) {
+  __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv) {
+    base = reinterpret_cast<const char*>(b);
+    ldb = ld * (int64_t)sizeof(T);
+    k_valid = kv;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int b = i * kThreads + (int)threadIdx.x;
-      const int rb = b % NRB, kb = b / NRB;
-      const int r = rb * RB;
-      const bool okb = (TOTAL % kThreads == 0 || b < TOTAL) && r < rows_valid;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int k = k0 + kb * 8 + kk;
-        v[i][kk] = (okb && k < k_valid) ? *reinterpret_cast<const uint2*>(base + (int64_t)k * ld + r)
-                                        : make_uint2(0, 0);
-      }
+    for (int i = 0; i < NI; ++i) {
+      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
+      kr[i] = lin / ROWB;
+      const int slot = (lin % ROWB) / 16;
+      const int r = (slot ^ swz(kr[i])) * CE;
+      off[i] = r < rows_valid ? (uint32_t)(kr[i] * ldb + r * (int)sizeof(T)) : kOOB;
     }
   }
-  __device__ __forceinline__ void store(T* lds) const {
+  __device__ __forceinline__ void issue(char* stage, int k0) const {
+    const rsrc_t rs = make_rsrc(base + (int64_t)k0 * ldb);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int b = i * kThreads + (int)threadIdx.x;
-      if (!(TOTAL % kThreads == 0 || b < TOTAL)) continue;
-      const int rb = b % NRB, kb = b / NRB;
-      const int r = rb * RB;
-      if constexpr (sizeof(T) == 2) {
-        // 8 k-rows x 4 elements -> 4 rows x 8 k-values (16 bytes each)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // element j of a k-row is the low (j even) or high (j odd) half of
-          // word x (j < 2) or y (j >= 2); pair k-rows 2p, 2p+1 into one word
-          uint32_t w[8];
-#pragma unroll
-          for (int kk = 0; kk < 8; ++kk) w[kk] = (j < 2) ? v[i][kk].x : v[i][kk].y;
-          uint32_t o[4];
-#pragma unroll
-          for (int p = 0; p < 4; ++p)
-            o[p] = (j & 1) ? ((w[2 * p] >> 16) | (w[2 * p + 1] & 0xffff0000u))
-                           : ((w[2 * p] & 0xffffu) | (w[2 * p + 1] << 16));
-          *reinterpret_cast<uint4*>(lds + (r + j) * LDR + kb * 8) = make_uint4(o[0], o[1], o[2], o[3]);
-        }
-      } else {
-        // 8 k-rows x 2 floats -> 2 rows x 8 k-values (32 bytes each)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          uint4 o0, o1;
-          o0.x = j ? v[i][0].y : v[i][0].x;
-          o0.y = j ? v[i][1].y : v[i][1].x;
-          o0.z = j ? v[i][2].y : v[i][2].x;
-          o0.w = j ? v[i][3].y : v[i][3].x;
-          o1.x = j ? v[i][4].y : v[i][4].x;
-          o1.y = j ? v[i][5].y : v[i][5].x;
-          o1.z = j ? v[i][6].y : v[i][6].x;
-          o1.w = j ? v[i][7].y : v[i][7].x;
-          uint4* dst = reinterpret_cast<uint4*>(lds + (r + j) * LDR + kb * 8);
-          dst[0] = o0;
-          dst[1] = o1;
-        }
-      }
+    for (int i = 0; i < NI; ++i) {
+      const uint32_t v = (off[i] == kOOB || k0 + kr[i] >= k_valid) ? kOOB : off[i];
+      dma16(rs, v, stage + (i * kThreads + wave_id() * 64) * 16);
     }
   }
 };
 
-// One LDS stage of C[FM][FN] += A_tile * B_tile^T for this wave: A rows
-// a_row0 .. a_row0 + 32*FM, B rows b_row0 .. b_row0 + 32*FN, BK reduction.
-template <class T, int BK, int FM, int FN>
-__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[FM][FN], const T* sA, const T* sB, int a_row0,
-                                          int b_row0) {
+// MFMA operand (8 reduction values of one row) from a staged tile.
+template <class T, int R, int BK>
+__device__ __forceinline__ typename Vec8<T>::type read_op(const KTile<T, R, BK>&, const char* stage, int row,
+                                                          int j) {
+  typedef KTile<T, R, BK> KT;
   typedef typename Vec8<T>::type V8;
-  constexpr int LDR = LdsRow<T, BK>::value;
   const int lane = lane_id();
-  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const int k = 16 * j + (lane >> 5) * 8;
+  const int c = k / KT::CE;
+  const char* rowp = stage + row * KT::ROWB;
+  if constexpr (sizeof(T) == 2) {
+    return *reinterpret_cast<const V8*>(rowp + ((c ^ KT::swz(row)) * 16));
+  } else {
+    const float4 lo = *reinterpret_cast<const float4*>(rowp + ((c ^ KT::swz(row)) * 16));
+    const float4 hi = *reinterpret_cast<const float4*>(rowp + (((c + 1) ^ KT::swz(row)) * 16));
+    V8 v;
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    return v;
+  }
+}
+
+template <class T, int R, int BK>
+__device__ __forceinline__ typename Vec8<T>::type read_op(const RTile<T, R, BK>&, const char* stage, int row,
+                                                          int j) {
+  typedef RTile<T, R, BK> RT;
+  typedef typename Vec8<T>::type V8;
+  const int lane = lane_id();
+  const int kb = 16 * j + (lane >> 5) * 8;
+  if constexpr (sizeof(T) == 2) {
+    // Transposing read: in each group of 16 lanes, lane 4a+q names row-chunk
+    // (k = kb + 4h + a, r = 16*group + 4q) and every lane receives 4 k-values
+    // of row (lane % 32).
+    const int g = (lane >> 4) & 1, a = (lane & 15) >> 2, q = lane & 3;
+    const int r = row - (lane & 31) + 16 * g + 4 * q;  // row is this lane's own row (m0 + lane % 32)
+    V8 out;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int krow = kb + 4 * h + a;
+      const char* p = stage + krow * RT::ROWB + (((r / RT::CE) ^ RT::swz(krow)) * 16) + (r % RT::CE) * 2;
+      const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const short sv = v[t];
+        T e;
+        __builtin_memcpy(&e, &sv, 2);
+        out[4 * h + t] = e;
+      }
+    }
+    return out;
+  } else {
+    V8 out;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int krow = kb + t;
+      out[t] = *reinterpret_cast<const float*>(stage + krow * RT::ROWB + (((row / RT::CE) ^ RT::swz(krow)) * 16) +
+                                               (row % RT::CE) * 4);
+    }
+    return out;
+  }
+}
+
+// Vocabulary operands packed once per call into the workspace, so every tile
+// load is aligned and in bounds: bias as fp32 [V_pad] (-inf past V: padding
+// rows drop out of the softmax) and E as [V_pad][DP] in the compute dtype
+// (zero past D and V).
+template <class T>
+__global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E, int64_t lde,
+                                                         const float* __restrict__ bias, int V, int D, int V_pad,
+                                                         int DP, T* __restrict__ Ep, float* __restrict__ biasp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < (int64_t)V_pad * DP) {
+    const int v = (int)(e / DP), d = (int)(e % DP);
+    Ep[e] = (v < V && d < D) ? E[(int64_t)v * lde + d] : (T)0.f;
+  }
+  if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
+}
+
+// acc[FM][FN] += A_stage[a_row0 + ...] * B_stage[b_row0 + ...]^T over one stage.
+template <class T, int BK, int FM, int FN, class TA, class TB>
+__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
+                                          const char* sB, int a_row0, int b_row0) {
+  typedef typename Vec8<T>::type V8;
+  const int lr = lane_id() & 31;
 #pragma unroll
   for (int j = 0; j < BK / 16; ++j) {
     V8 a[FM], b[FN];
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-      a[fm] = *reinterpret_cast<const V8*>(sA + (a_row0 + fm * 32 + lr) * LDR + j * 16 + lk);
+    for (int fm = 0; fm < FM; ++fm) a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-      b[fn] = *reinterpret_cast<const V8*>(sB + (b_row0 + fn * 32 + lr) * LDR + j * 16 + lk);
+    for (int fn = 0; fn < FN; ++fn) b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], a[fm], b[fn]);
   }
 }
-
-// Double-buffered reduction loop: acc += A[rows, 0:Kred] * B[rows, 0:Kred]^T.
-// `side` is called as side.pre(kt) before the stage's products (issue extra
-// global loads) and side.post(kt) after them (store those loads to LDS); all
-// threads pass a barrier after every stage, so side data written in stage kt
-// is visible from stage kt+1 on.  Ends with a barrier.
-template <class T, int BK, int FM, int FN, class TA, class TB, class Side>
-__device__ __forceinline__ void reduce_loop(f32x16_t (&acc)[FM][FN], TA& ta, TB& tb, T* sA0, T* sA1, T* sB0,
-                                            T* sB1, int k_total, int a_row0, int b_row0, Side& side) {
-  const int nk = (k_total + BK - 1) / BK;
-  if (nk > 0) {
-    ta.load(0);
-    tb.load(0);
-    ta.store(sA0);
-    tb.store(sB0);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool odd = kt & 1;
-    const T* cA = odd ? sA1 : sA0;
-    const T* cB = odd ? sB1 : sB0;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      ta.load((kt + 1) * BK);
-      tb.load((kt + 1) * BK);
-    }
-    side.pre(kt);
-    stage_mma<T, BK, FM, FN>(acc, cA, cB, a_row0, b_row0);
-    if (more) {
-      ta.store(odd ? sA0 : sA1);
-      tb.store(odd ? sB0 : sB1);
-    }
-    side.post(kt);
-    __syncthreads();
-  }
-}
-
-struct NoSide {
-  __device__ __forceinline__ void pre(int) {}
-  __device__ __forceinline__ void post(int) {}
-};
 
 // blockIdx -> tile index such that each XCD (blocks are dealt to the 8 XCDs
 // round-robin) works through a contiguous range of tile indices, so the tiles

@@ -22,76 +22,23 @@ namespace swvr {
 
 namespace {
 
-constexpr int kBK = 32;
-
-// E tile [BV][DP] (row stride DPE) and bias tile [BV], loaded during the
-// first stages of the tile's reduction loop.
-template <class T, int BV, int DP, int DPE>
-struct FwdSide {
-  static constexpr int PER = 8;
-  static constexpr int TOTAL = BV * DP;
-  static constexpr int BATCH = kThreads * PER;
-  static constexpr int ITERS = (TOTAL + BATCH - 1) / BATCH;
-  T* sE;
-  float* sBias;
-  const T* E;
-  int64_t lde;
-  const float* bias;
-  int v0, V, D;
-  T ev[PER];
-  float bv;
-
-  __device__ __forceinline__ void load(int it) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = (it * PER + q) * kThreads + (int)threadIdx.x;
-      const int vv = e / DP, d = e % DP;
-      const bool ok = e < TOTAL && v0 + vv < V && d < D;
-      ev[q] = ok ? E[(int64_t)(v0 + vv) * lde + d] : (T)0.f;
-    }
-    if (it == 0 && (int)threadIdx.x < BV) {
-      const int v = v0 + (int)threadIdx.x;
-      bv = v < V ? (bias ? bias[v] : 0.f) : kNegInf;
-    }
-  }
-  __device__ __forceinline__ void store(int it) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int e = (it * PER + q) * kThreads + (int)threadIdx.x;
-      if (e < TOTAL) sE[(e / DP) * DPE + e % DP] = ev[q];
-    }
-    if (it == 0 && (int)threadIdx.x < BV) sBias[threadIdx.x] = bv;
-  }
-  __device__ __forceinline__ void pre(int kt) {
-    if (kt < ITERS) load(kt);
-  }
-  __device__ __forceinline__ void post(int kt) {
-    if (kt < ITERS) store(kt);
-  }
-  // Batches the reduction loop had no stage for (small K).
-  __device__ __forceinline__ void finish(int nk) {
-    if (nk < ITERS) {
-      for (int it = nk; it < ITERS; ++it) {
-        load(it);
-        store(it);
-      }
-      __syncthreads();
-    }
-  }
-};
-
 template <class T, int BV, int BM, int DP>
 __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
   typedef typename Vec8<T>::type V8;
-  constexpr int LDR = LdsRow<T, kBK>::value;
-  constexpr int DPE = DP + 16 / (int)sizeof(T);
-  constexpr int FV = BV / 64, FT = BM / 64;  // 32x32 blocks per wave (2x2 waves)
+  constexpr int kBK = SliceK<T>::value;
+  typedef KTile<T, BV, kBK> TA;  // W rows of the vocabulary tile
+  typedef KTile<T, BM, kBK> TB;  // h rows of the token block
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;
+  constexpr int FV = BV / 64, FT = BM / 64;  // 32x32 blocks per wave (2 x 2 waves)
   constexpr int DB = DP / 32;
+  typedef KTile<T, BV, DP> TE;    // E tile [BV][DP], swizzled like an operand tile
+  constexpr int EBYTES = TE::BYTES;
+  constexpr int BBYTES = BV * 4;
 
-  __shared__ __attribute__((aligned(16))) T sW[2][BV * LDR];
-  __shared__ __attribute__((aligned(16))) T sH[2][BM * LDR];
-  __shared__ __attribute__((aligned(16))) T sE[BV * DPE];
-  __shared__ float sBias[BV];
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB + EBYTES + BBYTES];
+  char* const sE = smem + kStages * SB;
+  const float* const sBias = reinterpret_cast<const float*>(sE + EBYTES);
 
   const int lane = lane_id(), w = wave_id();
   const int wv = w >> 1, wt = w & 1;
@@ -100,8 +47,8 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
   const int n0 = tb * BM;
   const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
   const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
-  const T* h = static_cast<const T*>(p.h);
   const T* W = static_cast<const T*>(p.W);
+  const T* Ep = static_cast<const T*>(p.Ep);
 
   float m[FT], l[FT];
   f32x16_t oacc[DB][FT];
@@ -113,39 +60,55 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
     for (int db = 0; db < DB; ++db) oacc[db][ft] = zero16();
   }
 
-  KTile<T, BV, kBK> ta;
-  ta.ld = p.ldw;
-  ta.k_valid = p.K;
-  KTile<T, BM, kBK> tbh;
-  tbh.base = h + (int64_t)n0 * p.ldh;
-  tbh.ld = p.ldh;
-  tbh.rows_valid = p.N - n0;
-  tbh.k_valid = p.K;
   const int nk = (p.K + kBK - 1) / kBK;
-
-  for (int vt = vt_begin; vt < vt_end; ++vt) {
-    const int v0 = vt * BV;
-    ta.base = W + (int64_t)v0 * p.ldw;
-    ta.rows_valid = p.V - v0;
-    FwdSide<T, BV, DP, DPE> side;
-    side.sE = sE;
-    side.sBias = sBias;
-    side.E = static_cast<const T*>(p.E);
-    side.lde = p.lde;
-    side.bias = p.bias;
-    side.v0 = v0;
-    side.V = p.V;
-    side.D = p.D;
-
-    f32x16_t sacc[FV][FT];
+  const int total = (vt_end - vt_begin) * nk;
+  TA ta;
+  ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
+  TB tbh;
+  tbh.setup(static_cast<const T*>(p.h) + (int64_t)n0 * p.ldh, p.ldh, p.N - n0, p.K);
+  auto issue = [&](int g) {
+    const int kt = g % nk;
+    if (kt == 0) {
+      const int v0 = (vt_begin + g / nk) * BV;
+      ta.rebase(W + (int64_t)v0 * p.ldw, p.V - v0);
+    }
+    char* st = smem + (g % kStages) * SB;
+    ta.issue(st, kt * kBK);
+    tbh.issue(st + TA::BYTES, kt * kBK);
+  };
 #pragma unroll
-    for (int fv = 0; fv < FV; ++fv)
-#pragma unroll
-      for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+  for (int g = 0; g < kStages - 1; ++g)
+    if (g < total) issue(g);
 
-    reduce_loop<T, kBK, FV, FT>(sacc, ta, tbh, sW[0], sW[1], sH[0], sH[1], p.K, wv * (BV / 2), wt * (BM / 2),
-                                side);
-    side.finish(nk);
+  f32x16_t sacc[FV][FT];
+  for (int g = 0; g < total; ++g) {
+    const int kt = g % nk;
+    const int ahead = total - 1 - g < kStages - 2 ? total - 1 - g : kStages - 2;
+    wait_stages<L, kStages>(ahead);
+    stage_barrier();
+    if (g + kStages - 1 < total) issue(g + kStages - 1);
+    if (kt == 0) {
+      // E and bias tiles of this vocabulary tile; every wave has finished the
+      // previous tile's epilogue (barrier above)
+      const int v0 = (vt_begin + g / nk) * BV;
+      TE te;
+      te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
+      te.issue(sE, 0);
+      if ((int)threadIdx.x * 16 < BBYTES)
+        dma16(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, (char*)sBias + w * 1024);
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+    }
+    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, smem + (g % kStages) * SB, smem + (g % kStages) * SB + TA::BYTES,
+                              wv * (BV / 2), wt * (BM / 2));
+    if (kt != nk - 1) continue;
+    if (nk < kStages) {
+      // short reduction: the E / bias loads may still be in flight
+      wait_vmcnt<0>();
+      stage_barrier();
+    }
 
     // ---- scores -> running softmax of this wave's half tile
     float mx[FT];
@@ -201,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
 #pragma unroll
           for (int tt = 0; tt < 8; ++tt) {
             const int vv = wv * (BV / 2) + fv * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-            av[db][tt] = sE[vv * DPE + db * 32 + (lane & 31)];
+            av[db][tt] = *reinterpret_cast<const T*>(sE + TE::elem(vv, db * 32 + (lane & 31)));
           }
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
@@ -238,25 +201,28 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
 // Merge the partial softmaxes in a fixed order: O = sum_p acc_p e^(m_p - M) /
 // sum_p l_p e^(m_p - M), LSE = M + log(...).  A row with every score -inf ends
 // with M = -inf, L = 0: O = NaN and LSE = -inf, as swvr/chunked.py:105 gives.
+// One thread per (d, n) with n fastest (coalesced partial reads); the d = 0
+// thread of a row also writes its LSE.
 __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restrict__ part_m,
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_acc, int n_part, int N,
                                                           int D, int DP, float* __restrict__ O,
                                                           float* __restrict__ lse) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int Dw = D > 0 ? D : 1;
+  if (e >= (int64_t)N * Dw) return;
+  const int d = (int)(e / N), n = (int)(e % N);
   float M = kNegInf;
   for (int q = 0; q < n_part; ++q) M = fmaxf(M, part_m[(int64_t)q * N + n]);
   const float shift = M == kNegInf ? 0.f : M;
-  float L = 0.f;
-  for (int q = 0; q < n_part; ++q) L += part_l[(int64_t)q * N + n] * expf(part_m[(int64_t)q * N + n] - shift);
-  for (int d = 0; d < D; ++d) {
-    float a = 0.f;
-    for (int q = 0; q < n_part; ++q)
-      a += part_acc[((int64_t)q * DP + d) * N + n] * expf(part_m[(int64_t)q * N + n] - shift);
-    O[(int64_t)n * D + d] = a / L;
+  float L = 0.f, a = 0.f;
+  for (int q = 0; q < n_part; ++q) {
+    const float wq = expf(part_m[(int64_t)q * N + n] - shift);
+    L += part_l[(int64_t)q * N + n] * wq;
+    if (d < D) a += part_acc[((int64_t)q * DP + d) * N + n] * wq;
   }
-  lse[n] = M + logf(L);
+  if (d < D) O[(int64_t)n * D + d] = a / L;
+  if (d == 0) lse[n] = M + logf(L);
 }
 
 template <class T, int BV, int BM, int DP>
@@ -269,12 +235,13 @@ hipError_t launch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stre
 }
 
 // Tile shape per (dtype, padded D): the per-wave score block and the acc^T
-// block share the register file, and E plus two K-slices of W and h share LDS.
+// block share the register file; four K-slices of W and h plus the E tile
+// share LDS (160 KB).
 template <class T, int DP>
 struct FwdTile {
   static constexpr bool wide = sizeof(T) == 2;
-  static constexpr int BV = wide ? (DP <= 128 ? 256 : 128) : 128;
-  static constexpr int BM = wide ? 128 : (DP <= 64 ? 128 : 64);
+  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
+  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
 };
 
 template <class T, int DP>
@@ -307,6 +274,19 @@ void tile_of(int DP, int* BV, int* BM) {
   }
 }
 
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+template <class T>
+hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
+  const int64_t n = (int64_t)plan.V_pad * plan.DP;
+  timing_begin(kKindPack, stream);
+  pack_vocab_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
+      static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP,
+      const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
+  timing_end(kKindPack, stream);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan) {
@@ -314,11 +294,14 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
   int BV, BM;
+  size_t tbytes;
   if (dtype == kF32) {
     if (DP > 128) return false;
     tile_of<float>(DP, &BV, &BM);
+    tbytes = 4;
   } else if (dtype == kBF16 || dtype == kF16) {
     tile_of<bf16_t>(DP, &BV, &BM);
+    tbytes = 2;
   } else {
     return false;
   }
@@ -327,6 +310,7 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   plan->DP = DP;
   plan->n_tb = (int)((N + BM - 1) / BM);
   plan->n_vt = (int)((V + BV - 1) / BV);
+  plan->V_pad = plan->n_vt * BV;
   // Enough workgroups to fill 256 CUs several times over, at least two
   // vocabulary tiles per split.
   int n_split = 1;
@@ -339,27 +323,44 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   }
   plan->n_split = n_split;
   plan->n_part = 2 * n_split;
-  const size_t per = (size_t)N * sizeof(float);
-  plan->ws_bytes = (size_t)plan->n_part * per * (2 + (size_t)DP) + 256;
+  size_t off = 0;
+  plan->off_m = off;
+  off += align256((size_t)plan->n_part * N * 4);
+  plan->off_l = off;
+  off += align256((size_t)plan->n_part * N * 4);
+  plan->off_acc = off;
+  off += align256((size_t)plan->n_part * N * 4 * DP);
+  plan->off_Ep = off;
+  off += align256((size_t)plan->V_pad * DP * tbytes);
+  plan->off_bias = off;
+  off += align256((size_t)plan->V_pad * 4);
+  plan->ws_bytes = off;
   return true;
 }
 
-hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, float* O, float* lse, hipStream_t stream) {
+hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse,
+                      hipStream_t stream) {
   if (p.N == 0) return hipSuccess;
   p.n_tb = plan.n_tb;
   p.n_split = plan.n_split;
   p.n_vt = plan.n_vt;
+  p.part_m = reinterpret_cast<float*>(ws + plan.off_m);
+  p.part_l = reinterpret_cast<float*>(ws + plan.off_l);
+  p.part_acc = reinterpret_cast<float*>(ws + plan.off_acc);
+  p.Ep = ws + plan.off_Ep;
+  p.biasp = reinterpret_cast<const float*>(ws + plan.off_bias);
   hipError_t e;
   switch (dtype) {
-    case kBF16: e = dispatch_dp<bf16_t>(plan, p, stream); break;
-    case kF16: e = dispatch_dp<f16_t>(plan, p, stream); break;
-    case kF32: e = dispatch_dp<float>(plan, p, stream); break;
+    case kBF16: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, p, stream); break;
+    case kF16: e = pack<f16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<f16_t>(plan, p, stream); break;
+    case kF32: e = pack<float>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<float>(plan, p, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
   timing_begin(kKindFwdCombine, stream);
-  fwd_combine_kernel<<<(p.N + 255) / 256, 256, 0, stream>>>(p.part_m, p.part_l, p.part_acc, plan.n_part, p.N, p.D,
-                                                             plan.DP, O, lse);
+  const int64_t n_threads = (int64_t)p.N * (p.D > 0 ? p.D : 1);
+  fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(p.part_m, p.part_l, p.part_acc, plan.n_part,
+                                                                         p.N, p.D, plan.DP, O, lse);
   timing_end(kKindFwdCombine, stream);
   return hipGetLastError();
 }

@@ -15,6 +15,7 @@ enum KernelKind {
   kKindBwdGemm,
   kKindBwdReduce,
   kKindFill,
+  kKindPack,
   kNumKinds
 };
 
@@ -34,21 +35,25 @@ struct FwdParams {
   float scale;
   int N, K, V, D;
   int n_tb, n_split, n_vt;
-  float* part_m;    // [n_part][N]
-  float* part_l;    // [n_part][N]
-  float* part_acc;  // [n_part][DP][N]
+  float* part_m;       // [n_part][N]
+  float* part_l;       // [n_part][N]
+  float* part_acc;     // [n_part][DP][N]
+  const void* Ep;      // packed E [V_pad][DP], compute dtype
+  const float* biasp;  // packed bias [V_pad], -inf past V
 };
 
 struct FwdPlan {
   int BV, BM, DP;
   int n_tb, n_vt, n_split, n_part;
-  size_t ws_bytes;
+  int V_pad;
+  size_t off_m, off_l, off_acc, off_Ep, off_bias, ws_bytes;
 };
 
 // Tile shape, split count and workspace for a forward call; ok=false if the
 // dtype / D combination is unsupported.
 bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan);
-hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, float* O, float* lse, hipStream_t stream);
+hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse,
+                      hipStream_t stream);
 
 // ---------------------------------------------------------------- backward
 struct BwdPlan {
@@ -61,7 +66,8 @@ struct BwdPlan {
   int n_chunks;
   int G;                 // token groups of the dS kernel (dE / db partials)
   bool dh_acc;           // dh needs an fp32 accumulator across chunks
-  size_t off_delta, off_stage, off_pe, off_pb, off_dh, ws_bytes;
+  int V_pad;             // vocabulary rows of the packed E / bias
+  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_lsed, off_Ep, off_bias, ws_bytes;
 };
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
