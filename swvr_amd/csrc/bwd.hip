@@ -112,12 +112,14 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
   const int tb_end = (int)((int64_t)(g + 1) * p.n_tb / p.G);
 
   // E and bias of the vocabulary tile: once per workgroup, ahead of the stages
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsE = lds0 + kStages * SB, ldsG = ldsE + TE::BYTES, ldsB = ldsG + TG::BYTES;
+  const uint32_t ldsL = ldsB + BV * 4;
   {
     TE te;
     te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP);
-    te.issue(sE, 0);
-    if ((int)threadIdx.x * 16 < BV * 4)
-      dma16(make_rsrc(p.biasp + vg0), (uint32_t)threadIdx.x * 16, (char*)sBias + w * 1024);
+    te.issue(ldsE, 0);
+    if ((int)threadIdx.x * 16 < BV * 4) dma_batch1(make_rsrc(p.biasp + vg0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
   }
 
   f32x16_t deacc[DB][FV];
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
       const int n0 = (tb_begin + gs / nk) * BM;
       ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
     }
-    char* st = smem + (gs % kStages) * SB;
+    const uint32_t st = lds0 + (gs % kStages) * SB;
     ta.issue(st, kt * kBK);
     tw.issue(st + TA::BYTES, kt * kBK);
   };
@@ -158,17 +160,16 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
     const int ahead = total - 1 - gs < kStages - 2 ? total - 1 - gs : kStages - 2;
     wait_stages<L, kStages>(ahead);
     stage_barrier();
-    if (gs + kStages - 1 < total) issue(gs + kStages - 1);
     if (kt == 0) {
       // gO, LSE and delta of this token block; every wave has finished the
       // previous block's epilogue (barrier above)
       TG tg;
       tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
-      tg.issue(sG, 0);
+      tg.issue(ldsG, 0);
       const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
       if (c < BM / 2) {
         const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
-        dma16(make_rsrc(p.lsed), off, (char*)sLse + w * 1024);
+        dma_batch1(make_rsrc(p.lsed), off, ldsL + w * 1024);
       }
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft)
@@ -176,7 +177,9 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
         for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
     }
     const char* st = smem + (gs % kStages) * SB;
-    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, 0, w * WVR);
+    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, 0, w * WVR, [&] {
+      if (gs + kStages - 1 < total) issue(gs + kStages - 1);
+    });
     if (kt != nk - 1) continue;
     if (nk < kStages || gs < kStages) {
       // short reduction, or the first block (E / bias were issued before the
@@ -322,35 +325,50 @@ __device__ __forceinline__ void gemm_loop(f32x16_t (&acc)[FM][FN], const TA& ta,
   constexpr int SB = TA::BYTES + TB::BYTES;
   constexpr int L = TA::NI + TB::NI;
   const int nk = (k_total + BK - 1) / BK;
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int gs) {
+    const uint32_t st = lds0 + (gs % kStages) * SB;
+    ta.issue(st, gs * BK);
+    tb.issue(st + TA::BYTES, gs * BK);
+  };
 #pragma unroll
   for (int gs = 0; gs < kStages - 1; ++gs)
-    if (gs < nk) {
-      ta.issue(smem + gs * SB, gs * BK);
-      tb.issue(smem + gs * SB + TA::BYTES, gs * BK);
-    }
+    if (gs < nk) issue(gs);
   for (int gs = 0; gs < nk; ++gs) {
     const int ahead = nk - 1 - gs < kStages - 2 ? nk - 1 - gs : kStages - 2;
     wait_stages<L, kStages>(ahead);
     stage_barrier();
-    if (gs + kStages - 1 < nk) {
-      char* st = smem + ((gs + kStages - 1) % kStages) * SB;
-      ta.issue(st, (gs + kStages - 1) * BK);
-      tb.issue(st + TA::BYTES, (gs + kStages - 1) * BK);
-    }
     const char* st = smem + (gs % kStages) * SB;
-    stage_mma<T, BK, FM, FN>(acc, ta, tb, st, st + TA::BYTES, a_row0, b_row0);
+    stage_mma<T, BK, FM, FN>(acc, ta, tb, st, st + TA::BYTES, a_row0, b_row0, [&] {
+      if (gs + kStages - 1 < nk) issue(gs + kStages - 1);
+    });
   }
 }
+
+// Tile of the gradient GEMMs: GM x GN per workgroup of WM x WN waves
+// (two waves per SIMD for bf16 / f16, so one wave's LDS and barrier waits
+// are covered by the other's matrix work).
+template <class T>
+struct GemmTile {
+  static constexpr bool wide = sizeof(T) == 2;
+  static constexpr int GM = wide ? 256 : 128;
+  static constexpr int GN = GM;
+  static constexpr int WM = 2;
+  static constexpr int WN = wide ? 4 : 2;
+  static constexpr int NT = 64 * WM * WN;
+};
 
 // One tile of one gradient product; DW selects the product:
 //   DW:  dW[v0+v][k]  = sum_tok stage[v][tok] h[tok][k]     (A: KTile, B: RTile)
 //   !DW: dh[tok][k]  += sum_v  stage[v][tok] W[v0+v][k]      (A: RTile, B: RTile)
-template <class T, int GM, int GN, bool DW>
+template <class T, bool DW>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem) {
+  typedef GemmTile<T> G;
   constexpr int kBK = SliceK<T>::value;
-  constexpr int FM = GM / 64, FN = GN / 64;
+  constexpr int GM = G::GM, GN = G::GN, NT = G::NT;
+  constexpr int FM = GM / (32 * G::WM), FN = GN / (32 * G::WN);
   const int w = wave_id();
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / G::WN, wn = w % G::WN;
   const int mt = t / p.n_n, nt = t % p.n_n;
   const T* stage = static_cast<const T*>(p.stage);
   f32x16_t acc[FM][FN];
@@ -358,21 +376,21 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = zero16();
-  RTile<T, GN, kBK> tb;
+  RTile<T, GN, kBK, NT> tb;
   if constexpr (DW) {
-    KTile<T, GM, kBK> ta;
+    KTile<T, GM, kBK, NT> ta;
     ta.setup(stage + (int64_t)mt * GM * p.ld_stage, p.ld_stage, p.cv - mt * GM, p.N);
     tb.setup(static_cast<const T*>(p.h) + nt * GN, p.ldh, p.K - nt * GN, p.N);
-    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.N, wm * (GM / 2), wn * (GN / 2));
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.N, wm * (GM / G::WM), wn * (GN / G::WN));
   } else {
-    RTile<T, GM, kBK> ta;
+    RTile<T, GM, kBK, NT> ta;
     ta.setup(stage + (int64_t)mt * GM, p.ld_stage, (int)(p.N_pad - (int64_t)mt * GM), p.cv);
     tb.setup(static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);
-    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / 2), wn * (GN / 2));
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / G::WM), wn * (GN / G::WN));
   }
   const int rows = DW ? p.cv : p.N;
-  const int row0 = mt * GM + wm * (GM / 2);
-  const int col0 = nt * GN + wn * (GN / 2);
+  const int row0 = mt * GM + wm * (GM / G::WM);
+  const int col0 = nt * GN + wn * (GN / G::WN);
   // dispatch on the output dtype outside the unrolled store loops
   if constexpr (DW) {
     if (p.gW_dtype == kBF16)
@@ -397,17 +415,19 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
 // One launch covers both gradient products of a chunk: blocks [0, n_dw) are
 // dW tiles, blocks [n_dw, n_dw + n_dh) dh tiles.  The dW tiles (the longer
 // reduction, over all tokens) are dealt first.
-template <class T, int GM, int GN>
-__global__ __launch_bounds__(kThreads) void bwd_gemm_kernel(GemmParams p) {
+template <class T>
+__global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p) {
+  typedef GemmTile<T> G;
   constexpr int kBK = SliceK<T>::value;
-  constexpr int SB = KTile<T, GM, kBK>::BYTES + RTile<T, GN, kBK>::BYTES;
-  static_assert(KTile<T, GM, kBK>::BYTES == RTile<T, GM, kBK>::BYTES, "both A layouts stage the same bytes");
+  constexpr int SB = KTile<T, G::GM, kBK, G::NT>::BYTES + RTile<T, G::GN, kBK, G::NT>::BYTES;
+  static_assert(KTile<T, G::GM, kBK, G::NT>::BYTES == RTile<T, G::GM, kBK, G::NT>::BYTES,
+                "both A layouts stage the same bytes");
   __shared__ __attribute__((aligned(1024))) char smem[kStages * SB];
   const int b = blockIdx.x;
   if (b < p.n_dw)
-    gemm_tile<T, GM, GN, true>(p, xcd_swizzle(b, p.n_dw), smem);
+    gemm_tile<T, true>(p, xcd_swizzle(b, p.n_dw), smem);
   else
-    gemm_tile<T, GM, GN, false>(p, xcd_swizzle(b - p.n_dw, p.n_dh), smem);
+    gemm_tile<T, false>(p, xcd_swizzle(b - p.n_dw, p.n_dh), smem);
 }
 
 // ---------------------------------------------------------------- dE / db
@@ -468,12 +488,6 @@ struct ScoresTile {
   static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
 };
 
-template <class T>
-struct GemmTile {
-  static constexpr int GM = sizeof(T) == 2 ? 256 : 128;
-  static constexpr int GN = GM;
-};
-
 template <class T, int DP>
 hipError_t dispatch_scores_tile(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   typedef ScoresTile<T, DP> C;
@@ -500,7 +514,7 @@ hipError_t dispatch_gemm(const BwdPlan& plan, const GemmParams& gp, hipStream_t 
   if (blocks == 0) return hipSuccess;
   if (plan.GM != GemmTile<T>::GM || plan.GN != GemmTile<T>::GN) return hipErrorInvalidValue;
   timing_begin(kKindBwdGemm, stream);
-  bwd_gemm_kernel<T, GemmTile<T>::GM, GemmTile<T>::GN><<<blocks, kThreads, 0, stream>>>(gp);
+  bwd_gemm_kernel<T><<<blocks, GemmTile<T>::NT, 0, stream>>>(gp);
   timing_end(kKindBwdGemm, stream);
   return hipGetLastError();
 }

@@ -102,10 +102,15 @@ constexpr uint32_t kOOB = 0x80000000u;
 // (64-byte rows) for f32, which keeps the four-stage ring inside LDS.
 template <class T> struct SliceK { static constexpr int value = sizeof(T) == 2 ? 32 : 16; };
 
-// XOR swizzle of the 16-byte chunks of an LDS row of `cpr` chunks: the eight
-// rows that a ds_read_b128 serves in one pass land on distinct banks.
+// XOR swizzle of the 16-byte chunks of an LDS row of `cpr` chunks.  The
+// gfx950 LDS has 64 four-byte banks (256 bytes per cycle) and serves a
+// ds_read_b128 sixteen consecutive lanes per cycle; the operand reads have
+// those sixteen lanes on sixteen consecutive rows at the same logical chunk,
+// so the sixteen rows must land on sixteen distinct 16-byte bank groups.
 __device__ __forceinline__ int chunk_swizzle(int row, int cpr) {
-  return cpr >= 8 ? (row & 7) : (row / (8 / cpr)) % cpr;
+  const int rows_per_256 = cpr >= 16 ? 1 : 16 / cpr;
+  const int span = cpr >= 16 ? 16 : cpr;
+  return (row / rows_per_256) % span;
 }
 
 // Raw buffer descriptor over [base, base + 2^31 - 1): stride 0, 32-bit data
@@ -121,23 +126,72 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
   return r;
 }
 
-// One 16-byte chunk per lane into LDS at wave_base + 16 * lane
-// (buffer_load_dwordx4 ... lds; M0 holds the wave's LDS base).  Issued from
-// inline assembly so that the compiler does not guard every later LDS read
-// with a wait for all outstanding loads: the reduction loops order these
-// loads themselves (wait_stages + stage_barrier).  M0 is restored.
-__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, void* wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(size_t)(__attribute__((address_space(3))) char*)wave_base);
+// Wave-uniform LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const char*)p);
+}
+
+// buffer_load_dwordx4 ... lds: one 16-byte chunk per lane into LDS; load i of
+// a batch lands at lds + i * 4096 + 16 * lane (M0 holds the LDS base; it is
+// saved and restored around the batch).  Issued from inline assembly so that
+// the compiler does not guard every later LDS read with a wait for all
+// outstanding loads: the reduction loops order these loads themselves
+// (wait_stages + stage_barrier).
+__device__ __forceinline__ void dma_batch1(rsrc_t r, uint32_t v0, uint32_t lds_any) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_any);
   uint32_t save;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
       "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(save)
-      : "v"(voff), "s"(r), "s"(lds)
+      : "v"(v0), "s"(r), "s"(lds)
       : "memory");
+}
+template <int STEP>
+__device__ __forceinline__ void dma_batch2(rsrc_t r, uint32_t v0, uint32_t v1, uint32_t lds) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %4\n\t"
+      "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %5\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(v0), "v"(v1), "s"(r), "s"(lds), "i"(STEP)
+      : "memory");
+}
+template <int STEP>
+__device__ __forceinline__ void dma_batch4(rsrc_t r, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                           uint32_t lds) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %6\n\t"
+      "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %7\n\t"
+      "buffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %7\n\t"
+      "buffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
+      "s_add_u32 m0, m0, %7\n\t"
+      "buffer_load_dwordx4 %4, %5, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(r), "s"(lds), "i"(STEP)
+      : "memory");
+}
+// NI loads of one thread, STEP bytes apart in LDS starting at lds.
+template <int NI, int STEP>
+__device__ __forceinline__ void dma_n(rsrc_t r, const uint32_t (&v)[NI], uint32_t lds_any) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_any);  // wave-uniform by construction
+  if constexpr (NI == 1) {
+    dma_batch1(r, v[0], lds);
+  } else if constexpr (NI == 2) {
+    dma_batch2<STEP>(r, v[0], v[1], lds);
+  } else {
+    static_assert(NI % 4 == 0, "batches of 4");
+#pragma unroll
+    for (int i = 0; i < NI; i += 4) dma_batch4<STEP>(r, v[i], v[i + 1], v[i + 2], v[i + 3], lds + i * STEP);
+  }
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
@@ -167,14 +221,14 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     wait_vmcnt<0>();
 }
 
-template <class T, int R, int BK>
+template <class T, int R, int BK, int NT = kThreads>
 struct KTile {
   static constexpr int CE = 16 / (int)sizeof(T);    // elements per chunk
   static constexpr int CPR = BK / CE;               // chunks per LDS row
   static constexpr int ROWB = BK * (int)sizeof(T);  // bytes per LDS row
   static constexpr int BYTES = R * ROWB;
-  static constexpr int NI = BYTES / (kThreads * 16);  // loads per thread per stage
-  static_assert(BYTES % (kThreads * 16) == 0, "tile must be a whole number of wave loads");
+  static constexpr int NI = BYTES / (NT * 16);      // loads per thread per stage
+  static_assert(BYTES % (NT * 16) == 0, "tile must be a whole number of workgroup loads");
   static_assert(CPR >= 4 && (CPR & (CPR - 1)) == 0, "rows of 4, 8, 16, ... chunks");
 
   __device__ static __forceinline__ int swz(int row) { return chunk_swizzle(row, CPR); }
@@ -182,61 +236,66 @@ struct KTile {
   __device__ static __forceinline__ int elem(int row, int col) {
     return row * ROWB + (((col / CE) ^ swz(row)) * 16) + (col % CE) * (int)sizeof(T);
   }
+  // Row and first reduction index of this lane's chunk of load i.
+  __device__ static __forceinline__ int row_of(int i) { return ((i * NT + (int)threadIdx.x) * 16) / ROWB; }
+  __device__ static __forceinline__ int kc_of(int i) {
+    const int lin = (i * NT + (int)threadIdx.x) * 16;
+    return (((lin % ROWB) / 16) ^ swz(lin / ROWB)) * CE;
+  }
 
   const char* base;  // element (0, 0)
   int64_t ldb;       // row stride in bytes
-  uint32_t off[NI];  // byte offset of this lane's chunk at k = 0, or kOOB
-  int kc[NI];        // first reduction index of the chunk
   int k_valid;
+  uint32_t off[NI];  // byte offset of this lane's chunk at k = 0, or kOOB
 
   __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv) {
-    base = reinterpret_cast<const char*>(b);
     ldb = ld * (int64_t)sizeof(T);
     k_valid = kv;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
-      const int row = lin / ROWB, slot = (lin % ROWB) / 16;
-      kc[i] = (slot ^ swz(row)) * CE;
-      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc[i] * (int)sizeof(T)) : kOOB;
-    }
+    rebase(b, rows_valid);
   }
-  // New rows, same shape (the per-lane offsets only depend on rows_valid).
+  // New rows, same shape.
   __device__ __forceinline__ void rebase(const T* b, int rows_valid) {
     base = reinterpret_cast<const char*>(b);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
-      const int row = lin / ROWB;
-      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc[i] * (int)sizeof(T)) : kOOB;
+      const int row = row_of(i);
+      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc_of(i) * (int)sizeof(T)) : kOOB;
     }
   }
-  __device__ __forceinline__ void issue(char* stage, int k0) const {
+  // Stage the reduction slice [k0, k0 + BK) at LDS address lds.
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
     const rsrc_t r = make_rsrc(base + (int64_t)k0 * (int)sizeof(T));
+    uint32_t v[NI];
+    if (k0 + BK <= k_valid) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const uint32_t v = (off[i] == kOOB || k0 + kc[i] >= k_valid) ? kOOB : off[i];
-      dma16(r, v, stage + (i * kThreads + wave_id() * 64) * 16);
+      for (int i = 0; i < NI; ++i) v[i] = off[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) v[i] = k0 + kc_of(i) >= k_valid ? kOOB : off[i];
     }
+    dma_n<NI, NT * 16>(r, v, lds + wave_id() * 1024);
   }
 };
 
-template <class T, int R, int BK>
+template <class T, int R, int BK, int NT = kThreads>
 struct RTile {
   static constexpr int CE = 16 / (int)sizeof(T);
   static constexpr int ROWB = R * (int)sizeof(T);  // bytes per LDS k-row
   static constexpr int BYTES = BK * ROWB;
-  static constexpr int NI = BYTES / (kThreads * 16);
-  static_assert(BYTES % (kThreads * 16) == 0, "tile must be a whole number of wave loads");
-  static_assert(ROWB >= 128, "swizzle needs 8 chunks per k-row");
+  static constexpr int NI = BYTES / (NT * 16);
+  static_assert(BYTES % (NT * 16) == 0, "tile must be a whole number of workgroup loads");
+  static_assert(ROWB >= 256, "swizzle needs 16 chunks per k-row");
 
-  __device__ static __forceinline__ int swz(int krow) { return (krow & 3) * 2; }
+  // The transposing read of a k16 step covers 4 k-rows x 64 bytes per 32
+  // lanes; XOR-ing the chunk index by 4 * (k-row % 4) puts those 4 x 64 bytes
+  // on all 64 banks.
+  __device__ static __forceinline__ int swz(int krow) { return (krow & 3) * 4; }
+  __device__ static __forceinline__ int kr_of(int i) { return ((i * NT + (int)threadIdx.x) * 16) / ROWB; }
 
   const char* base;  // element (r = 0, k = 0)
   int64_t ldb;       // k-row stride in bytes
-  uint32_t off[NI];
-  int kr[NI];        // k-row of the chunk within the stage
   int k_valid;
+  uint32_t off[NI];
 
   __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv) {
     base = reinterpret_cast<const char*>(b);
@@ -244,28 +303,31 @@ struct RTile {
     k_valid = kv;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int lin = (i * kThreads + (int)threadIdx.x) * 16;
-      kr[i] = lin / ROWB;
-      const int slot = (lin % ROWB) / 16;
-      const int r = (slot ^ swz(kr[i])) * CE;
-      off[i] = r < rows_valid ? (uint32_t)(kr[i] * ldb + r * (int)sizeof(T)) : kOOB;
+      const int lin = (i * NT + (int)threadIdx.x) * 16;
+      const int kr = lin / ROWB;
+      const int r = (((lin % ROWB) / 16) ^ swz(kr)) * CE;
+      off[i] = r < rows_valid ? (uint32_t)(kr * ldb + r * (int)sizeof(T)) : kOOB;
     }
   }
-  __device__ __forceinline__ void issue(char* stage, int k0) const {
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
     const rsrc_t rs = make_rsrc(base + (int64_t)k0 * ldb);
+    uint32_t v[NI];
+    if (k0 + BK <= k_valid) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const uint32_t v = (off[i] == kOOB || k0 + kr[i] >= k_valid) ? kOOB : off[i];
-      dma16(rs, v, stage + (i * kThreads + wave_id() * 64) * 16);
+      for (int i = 0; i < NI; ++i) v[i] = off[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) v[i] = k0 + kr_of(i) >= k_valid ? kOOB : off[i];
     }
+    dma_n<NI, NT * 16>(rs, v, lds + wave_id() * 1024);
   }
 };
 
 // MFMA operand (8 reduction values of one row) from a staged tile.
-template <class T, int R, int BK>
-__device__ __forceinline__ typename Vec8<T>::type read_op(const KTile<T, R, BK>&, const char* stage, int row,
+template <class T, int R, int BK, int NT>
+__device__ __forceinline__ typename Vec8<T>::type read_op(const KTile<T, R, BK, NT>&, const char* stage, int row,
                                                           int j) {
-  typedef KTile<T, R, BK> KT;
+  typedef KTile<T, R, BK, NT> KT;
   typedef typename Vec8<T>::type V8;
   const int lane = lane_id();
   const int k = 16 * j + (lane >> 5) * 8;
@@ -283,10 +345,10 @@ __device__ __forceinline__ typename Vec8<T>::type read_op(const KTile<T, R, BK>&
   }
 }
 
-template <class T, int R, int BK>
-__device__ __forceinline__ typename Vec8<T>::type read_op(const RTile<T, R, BK>&, const char* stage, int row,
+template <class T, int R, int BK, int NT>
+__device__ __forceinline__ typename Vec8<T>::type read_op(const RTile<T, R, BK, NT>&, const char* stage, int row,
                                                           int j) {
-  typedef RTile<T, R, BK> RT;
+  typedef RTile<T, R, BK, NT> RT;
   typedef typename Vec8<T>::type V8;
   const int lane = lane_id();
   const int kb = 16 * j + (lane >> 5) * 8;
@@ -339,24 +401,33 @@ __global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E
   if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
 }
 
-// acc[FM][FN] += A_stage[a_row0 + ...] * B_stage[b_row0 + ...]^T over one stage.
-template <class T, int BK, int FM, int FN, class TA, class TB>
-__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
-                                          const char* sB, int a_row0, int b_row0) {
+// acc[FM][FN] += A_stage[a_row0 + ...] * B_stage[b_row0 + ...]^T over the
+// k16 step j of a staged slice.
+template <class T, int FM, int FN, class TA, class TB>
+__device__ __forceinline__ void stage_step(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
+                                           const char* sB, int a_row0, int b_row0, int j) {
   typedef typename Vec8<T>::type V8;
   const int lr = lane_id() & 31;
+  V8 a[FM], b[FN];
 #pragma unroll
-  for (int j = 0; j < BK / 16; ++j) {
-    V8 a[FM], b[FN];
+  for (int fm = 0; fm < FM; ++fm) a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
+  for (int fn = 0; fn < FN; ++fn) b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+  for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
+    for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], a[fm], b[fn]);
+}
+
+// One stage: the first k16 step, then `between` (the next stage's loads, so
+// that their issue overlaps the matrix work already in flight), then the rest.
+template <class T, int BK, int FM, int FN, class TA, class TB, class F>
+__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
+                                          const char* sB, int a_row0, int b_row0, F&& between) {
+  stage_step<T, FM, FN>(acc, ta, tb, sA, sB, a_row0, b_row0, 0);
+  between();
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], a[fm], b[fn]);
-  }
+  for (int j = 1; j < BK / 16; ++j) stage_step<T, FM, FN>(acc, ta, tb, sA, sB, a_row0, b_row0, j);
 }
 
 // blockIdx -> tile index such that each XCD (blocks are dealt to the 8 XCDs

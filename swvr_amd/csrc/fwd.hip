@@ -62,6 +62,8 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
 
   const int nk = (p.K + kBK - 1) / kBK;
   const int total = (vt_end - vt_begin) * nk;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsE = lds0 + kStages * SB, ldsB = ldsE + EBYTES;
   TA ta;
   ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
   TB tbh;
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
       const int v0 = (vt_begin + g / nk) * BV;
       ta.rebase(W + (int64_t)v0 * p.ldw, p.V - v0);
     }
-    char* st = smem + (g % kStages) * SB;
+    const uint32_t st = lds0 + (g % kStages) * SB;
     ta.issue(st, kt * kBK);
     tbh.issue(st + TA::BYTES, kt * kBK);
   };
@@ -86,23 +88,23 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
     const int ahead = total - 1 - g < kStages - 2 ? total - 1 - g : kStages - 2;
     wait_stages<L, kStages>(ahead);
     stage_barrier();
-    if (g + kStages - 1 < total) issue(g + kStages - 1);
     if (kt == 0) {
       // E and bias tiles of this vocabulary tile; every wave has finished the
       // previous tile's epilogue (barrier above)
       const int v0 = (vt_begin + g / nk) * BV;
       TE te;
       te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
-      te.issue(sE, 0);
-      if ((int)threadIdx.x * 16 < BBYTES)
-        dma16(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, (char*)sBias + w * 1024);
+      te.issue(ldsE, 0);
+      if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
 #pragma unroll
       for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
     }
-    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, smem + (g % kStages) * SB, smem + (g % kStages) * SB + TA::BYTES,
-                              wv * (BV / 2), wt * (BM / 2));
+    const char* st = smem + (g % kStages) * SB;
+    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * (BV / 2), wt * (BM / 2), [&] {
+      if (g + kStages - 1 < total) issue(g + kStages - 1);
+    });
     if (kt != nk - 1) continue;
     if (nk < kStages) {
       // short reduction: the E / bias loads may still be in flight
