@@ -75,25 +75,41 @@ struct ScoresParams {
   int need_stage, need_dE, need_db;
 };
 
+// Tile shape of the scores kernel per (dtype, padded D): BM tokens x BV
+// vocabulary rows per workgroup of WT x WV waves (two waves per SIMD for
+// bf16 / f16).  dE^T (DP x BV/WV per wave) and the score block share the
+// register file; the stage ring, E, and the gO tile share LDS.
+template <class T, int DP>
+struct ScoresTile {
+  static constexpr bool wide = sizeof(T) == 2;
+  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
+  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
+  static constexpr int WT = wide && DP == 128 ? 2 : 1;
+  static constexpr int WV = wide && DP <= 64 ? 8 : 4;
+  static constexpr int NT = 64 * WT * WV;
+};
+
 // One workgroup: BV vocabulary rows of the chunk x one group of token
-// blocks.  Waves split the BV rows four ways, so dE / db of a vocabulary row
-// live in one wave's registers for the whole group.  Scores use the S layout
-// (A = h rows, B = W rows): a lane holds one vocabulary column and the
-// registers hold tokens, which is the B-operand layout P needs for
-// dE^T = gO^T P.
-template <class T, int BM, int BV, int DP>
-__global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
+// blocks.  Each wave owns BV/WV vocabulary rows and BM/WT tokens of every
+// block, so dE / db of its rows accumulate in its registers for the whole
+// group (one partial per token-wave row).  Scores use the S layout (A = h
+// rows, B = W rows): a lane holds one vocabulary column and the registers
+// hold tokens, which is the B-operand layout P needs for dE^T = gO^T P.
+template <class T, int DP>
+__global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(ScoresParams p) {
+  typedef ScoresTile<T, DP> C;
   typedef typename Vec8<T>::type V8;
   constexpr int kBK = SliceK<T>::value;
-  typedef KTile<T, BM, kBK> TA;  // h rows of the token block
-  typedef KTile<T, BV, kBK> TB;  // W rows of the vocabulary tile
-  typedef KTile<T, BV, DP> TE;   // E tile
-  typedef KTile<T, BM, DP> TG;   // gO tile
+  constexpr int BM = C::BM, BV = C::BV, NT = C::NT;
+  constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
+  typedef KTile<T, BM, kBK, NT> TA;  // h rows of the token block
+  typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
+  typedef KTile<T, BV, DP, NT> TE;   // E tile
+  typedef KTile<T, BM, DP, NT> TG;   // gO tile
   constexpr int SB = TA::BYTES + TB::BYTES;
-  constexpr int L = TA::NI + TB::NI;
-  constexpr int FT = BM / 32, FV = BV / 128;
+  constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
+  constexpr int FT = WTR / 32, FV = WVR / 32;
   constexpr int DB = DP / 32, DK = DP / 16;
-  constexpr int WVR = BV / 4;  // vocabulary rows per wave
 
   __shared__ __attribute__((aligned(1024))) char smem[kStages * SB + TE::BYTES + TG::BYTES + BV * 4 + 2 * BM * 4];
   char* const sE = smem + kStages * SB;
@@ -103,6 +119,7 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
   float* const sDelta = sLse + BM;
 
   const int lane = lane_id(), w = wave_id();
+  const int wt = w / C::WV, wv = w % C::WV;
   const int t = xcd_swizzle(blockIdx.x, p.n_vtc * p.G);
   const int vt = t / p.G, g = t % p.G;
   const int vl0 = vt * BV;      // first chunk-local row of this tile
@@ -177,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
         for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
     }
     const char* st = smem + (gs % kStages) * SB;
-    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, 0, w * WVR, [&] {
+    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, wt * WTR, wv * WVR, [&] {
       if (gs + kStages - 1 < total) issue(gs + kStages - 1);
     });
     if (kt != nk - 1) continue;
@@ -192,29 +209,36 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
     TE tel;
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv) {
-      const int vl = w * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
+      const int vl = wv * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
       const float bvv = vl < rows ? sBias[vl] : kNegInf;
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
+        // LDS bases recomputed per block (see opaque_zero)
+        const int oz = opaque_zero();
+        const char* sGe = sG + oz;
+        const char* sEe = sE + oz;
+        const float* sLe = sLse + oz;
+        const float* sDe = sDelta + oz;
+        const int tr0 = wt * WTR + ft * 32;  // first token of the block
         // dP block = gO[tokens] E[rows]^T over D
         f32x16_t dp = zero16();
 #pragma unroll
         for (int kd = 0; kd < DK; ++kd)
-          mfma_k16(dp, read_op(tgl, sG, ft * 32 + (lane & 31), kd), read_op(tel, sE, vl, kd));
+          mfma_k16(dp, read_op(tgl, sGe, tr0 + (lane & 31), kd), read_op(tel, sEe, vl, kd));
         float dbs = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int tl = ft * 32 + c_row(r, lane);
+          const int tl = tr0 + c_row(r, lane);
           const float x = sacc[ft][fv][r] * p.scale + bvv;
-          const float pv = fast_exp(x - sLse[tl]);
-          const float ds = pv * (dp[r] - sDelta[tl]);
+          const float pv = fast_exp(x - sLe[tl]);
+          const float ds = pv * (dp[r] - sDe[tl]);
           dbs += ds;
           sacc[ft][fv][r] = pv;
           dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
         }
         dbacc[fv] += dbs;
         if (p.need_stage) {
-          T* dst = stage + (int64_t)(vl0 + vl) * p.ld_stage + n0 + ft * 32 + (lane >> 5) * 4;
+          T* dst = stage + (int64_t)(vl0 + vl) * p.ld_stage + n0 + tr0 + (lane >> 5) * 4;
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             if constexpr (sizeof(T) == 2) {
@@ -243,23 +267,26 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
               V8 av;
 #pragma unroll
               for (int tt = 0; tt < 8; ++tt) {
-                const int tl = ft * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-                av[tt] = *reinterpret_cast<const T*>(sG + TG::elem(tl, db * 32 + (lane & 31)));
+                const int tl = tr0 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
+                av[tt] = *reinterpret_cast<const T*>(sGe + TG::elem(tl, db * 32 + (lane & 31)));
               }
               mfma_k16(deacc[db][fv], av, bv);
             }
           }
         }
+        sched_fence();
       }
     }
   }
 
+  // partials of this wave's rows over its token share of the group
+  const int gp = g * C::WT + wt;
 #pragma unroll
   for (int fv = 0; fv < FV; ++fv) {
-    const int vc = vl0 + w * WVR + fv * 32 + (lane & 31);  // chunk-local row
+    const int vc = vl0 + wv * WVR + fv * 32 + (lane & 31);  // chunk-local row
     if (p.need_db) {
       const float s = wave_sum32(dbacc[fv]);
-      if (lane < 32) p.part_db[(int64_t)g * p.C + vc] = s;
+      if (lane < 32) p.part_db[(int64_t)gp * p.C + vc] = s;
     }
     if (p.need_dE) {
 #pragma unroll
@@ -267,7 +294,7 @@ __global__ __launch_bounds__(kThreads) void bwd_scores_kernel(ScoresParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int d = db * 32 + c_row(r, lane);
-          p.part_dE[((int64_t)g * DP + d) * p.C + vc] = deacc[db][fv][r];
+          p.part_dE[((int64_t)gp * DP + d) * p.C + vc] = deacc[db][fv][r];
         }
     }
   }
@@ -323,7 +350,7 @@ template <class T, int BK, int FM, int FN, class TA, class TB>
 __device__ __forceinline__ void gemm_loop(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, char* smem,
                                           int k_total, int a_row0, int b_row0) {
   constexpr int SB = TA::BYTES + TB::BYTES;
-  constexpr int L = TA::NI + TB::NI;
+  constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
   const int nk = (k_total + BK - 1) / BK;
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int gs) {
@@ -470,39 +497,24 @@ hipError_t fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <class T, int BM, int BV, int DP>
-hipError_t launch_scores(const ScoresParams& sp, hipStream_t stream) {
-  timing_begin(kKindBwdScores, stream);
-  bwd_scores_kernel<T, BM, BV, DP><<<sp.n_vtc * sp.G, kThreads, 0, stream>>>(sp);
-  timing_end(kKindBwdScores, stream);
-  return hipGetLastError();
-}
-
-// Tile shape of the scores kernel per (dtype, padded D): dE^T (DP x BV/4 per
-// wave) and the score block (BM x BV/4 per wave) share the register file; the
-// stage ring, E, and the gO tile share LDS.
 template <class T, int DP>
-struct ScoresTile {
-  static constexpr bool wide = sizeof(T) == 2;
-  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
-  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
-};
-
-template <class T, int DP>
-hipError_t dispatch_scores_tile(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
+hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   typedef ScoresTile<T, DP> C;
   if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
-  return launch_scores<T, C::BM, C::BV, DP>(sp, stream);
+  timing_begin(kKindBwdScores, stream);
+  bwd_scores_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+  timing_end(kKindBwdScores, stream);
+  return hipGetLastError();
 }
 
 template <class T>
 hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   switch (plan.DP) {
-    case 32: return dispatch_scores_tile<T, 32>(plan, sp, stream);
-    case 64: return dispatch_scores_tile<T, 64>(plan, sp, stream);
-    case 128: return dispatch_scores_tile<T, 128>(plan, sp, stream);
+    case 32: return launch_scores<T, 32>(plan, sp, stream);
+    case 64: return launch_scores<T, 64>(plan, sp, stream);
+    case 128: return launch_scores<T, 128>(plan, sp, stream);
     case 256:
-      if constexpr (sizeof(T) == 2) return dispatch_scores_tile<T, 256>(plan, sp, stream);
+      if constexpr (sizeof(T) == 2) return launch_scores<T, 256>(plan, sp, stream);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -607,7 +619,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if (p.gE || p.gb) {
       timing_begin(kKindBwdReduce, stream);
       const int64_t n_threads = (p.gE ? (int64_t)cv * p.D : 0) + (p.gb ? cv : 0);
-      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(part_dE, part_db, plan.G, (int)plan.C,
+      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(part_dE, part_db, plan.n_gpart, (int)plan.C,
                                                                             plan.DP, v0, cv, p.D, p.gE, p.gE_dtype,
                                                                             p.gb);
       timing_end(kKindBwdReduce, stream);
@@ -617,13 +629,20 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   return hipSuccess;
 }
 
+template <class T, int DP>
+void scores_get(int* BM, int* BV, int* WT) {
+  *BM = ScoresTile<T, DP>::BM;
+  *BV = ScoresTile<T, DP>::BV;
+  *WT = ScoresTile<T, DP>::WT;
+}
+
 template <class T>
-void scores_tile_of(int DP, int* BM, int* BV) {
+void scores_tile_of(int DP, int* BM, int* BV, int* WT) {
   switch (DP) {
-    case 32: *BM = ScoresTile<T, 32>::BM; *BV = ScoresTile<T, 32>::BV; break;
-    case 64: *BM = ScoresTile<T, 64>::BM; *BV = ScoresTile<T, 64>::BV; break;
-    case 128: *BM = ScoresTile<T, 128>::BM; *BV = ScoresTile<T, 128>::BV; break;
-    default: *BM = ScoresTile<T, 256>::BM; *BV = ScoresTile<T, 256>::BV; break;
+    case 32: scores_get<T, 32>(BM, BV, WT); break;
+    case 64: scores_get<T, 64>(BM, BV, WT); break;
+    case 128: scores_get<T, 128>(BM, BV, WT); break;
+    default: scores_get<T, 256>(BM, BV, WT); break;
   }
 }
 
@@ -636,14 +655,14 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan) {
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
-  int BM, BV, GM, GN;
+  int BM, BV, GM, GN, WT;
   if (dtype == kF32) {
     if (DP > 128) return false;
-    scores_tile_of<float>(DP, &BM, &BV);
+    scores_tile_of<float>(DP, &BM, &BV, &WT);
     GM = GemmTile<float>::GM;
     GN = GemmTile<float>::GN;
   } else if (dtype == kBF16 || dtype == kF16) {
-    scores_tile_of<bf16_t>(DP, &BM, &BV);
+    scores_tile_of<bf16_t>(DP, &BM, &BV, &WT);
     GM = GemmTile<bf16_t>::GM;
     GN = GemmTile<bf16_t>::GN;
   } else {
@@ -667,6 +686,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G > plan->n_tb) G = plan->n_tb;
   if (G < 1) G = 1;
   plan->G = G;
+  plan->n_gpart = G * WT;  // dE / db partials: one per token group and token-wave row
   plan->dh_acc = need_gh && plan->n_chunks > 1;
   plan->V_pad = ((V + BV - 1) / BV) * BV;
   const size_t tb = dtype_bytes(dtype);
@@ -674,9 +694,9 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->off_stage = off;
   off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pe = off;
-  off += align256((size_t)G * DP * c * 4);
+  off += align256((size_t)plan->n_gpart * DP * c * 4);
   plan->off_pb = off;
-  off += align256((size_t)G * c * 4);
+  off += align256((size_t)plan->n_gpart * c * 4);
   plan->off_dh = off;
   if (plan->dh_acc) off += align256((size_t)N * K * 4);
   plan->off_gO = off;

@@ -209,6 +209,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // compiler from moving memory accesses across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Compiler-only fence: keeps the scheduler from hoisting the LDS reads of a
+// later epilogue block above this point (which would keep them all live).
+__device__ __forceinline__ void sched_fence() { asm volatile("" ::: "memory"); }
+
+// A zero the compiler cannot see through.  Added to LDS gather addresses in
+// an epilogue, it stops loop-invariant code motion from hoisting dozens of
+// gather addresses out of the tile loop and keeping them live (spills).
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 // Wait until at most `ahead` stages of L loads per thread are outstanding.
 template <int L, int NS>
 __device__ __forceinline__ void wait_stages(int ahead) {
@@ -227,8 +240,13 @@ struct KTile {
   static constexpr int CPR = BK / CE;               // chunks per LDS row
   static constexpr int ROWB = BK * (int)sizeof(T);  // bytes per LDS row
   static constexpr int BYTES = R * ROWB;
-  static constexpr int NI = BYTES / (NT * 16);      // loads per thread per stage
-  static_assert(BYTES % (NT * 16) == 0, "tile must be a whole number of workgroup loads");
+  static constexpr int NI = (BYTES + NT * 16 - 1) / (NT * 16);  // loads per thread per stage
+  // A tile smaller than one load per thread is loaded by the first BYTES/1024
+  // waves only.
+  static constexpr bool PARTIAL = BYTES < NT * 16;
+  static_assert(PARTIAL ? BYTES % 1024 == 0 : BYTES % (NT * 16) == 0, "tile must be whole wave loads");
+  // Loads every thread issues per stage (what a vmcnt wait may count on).
+  static constexpr int NI_MIN = PARTIAL ? 0 : NI;
   static_assert(CPR >= 4 && (CPR & (CPR - 1)) == 0, "rows of 4, 8, 16, ... chunks");
 
   __device__ static __forceinline__ int swz(int row) { return chunk_swizzle(row, CPR); }
@@ -259,7 +277,7 @@ struct KTile {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int row = row_of(i);
-      off[i] = row < rows_valid ? (uint32_t)(row * ldb + kc_of(i) * (int)sizeof(T)) : kOOB;
+      off[i] = row < rows_valid && row < R ? (uint32_t)(row * ldb + kc_of(i) * (int)sizeof(T)) : kOOB;
     }
   }
   // Stage the reduction slice [k0, k0 + BK) at LDS address lds.
@@ -273,6 +291,7 @@ struct KTile {
 #pragma unroll
       for (int i = 0; i < NI; ++i) v[i] = k0 + kc_of(i) >= k_valid ? kOOB : off[i];
     }
+    if (PARTIAL && (int)threadIdx.x * 16 >= BYTES) return;  // wave-uniform
     dma_n<NI, NT * 16>(r, v, lds + wave_id() * 1024);
   }
 };
@@ -283,6 +302,7 @@ struct RTile {
   static constexpr int ROWB = R * (int)sizeof(T);  // bytes per LDS k-row
   static constexpr int BYTES = BK * ROWB;
   static constexpr int NI = BYTES / (NT * 16);
+  static constexpr int NI_MIN = NI;
   static_assert(BYTES % (NT * 16) == 0, "tile must be a whole number of workgroup loads");
   static_assert(ROWB >= 256, "swizzle needs 16 chunks per k-row");
 

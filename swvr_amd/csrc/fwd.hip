@@ -22,17 +22,34 @@ namespace swvr {
 
 namespace {
 
-template <class T, int BV, int BM, int DP>
-__global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
+// Tile shape per (dtype, padded D): BV vocabulary rows x BM tokens per
+// workgroup of WV x WT waves (two waves per SIMD for bf16 / f16); the
+// per-wave score block and acc^T block share the register file, four
+// K-slices of W and h plus the E tile share LDS (160 KB).
+template <class T, int DP>
+struct FwdTile {
+  static constexpr bool wide = sizeof(T) == 2;
+  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
+  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
+  static constexpr int WV = wide ? (DP == 128 ? 2 : 4) : 2;
+  static constexpr int WT = wide ? (DP == 128 ? 4 : 2) : 2;
+  static constexpr int NT = 64 * WV * WT;
+};
+
+template <class T, int DP>
+__global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParams p) {
+  typedef FwdTile<T, DP> C;
   typedef typename Vec8<T>::type V8;
   constexpr int kBK = SliceK<T>::value;
-  typedef KTile<T, BV, kBK> TA;  // W rows of the vocabulary tile
-  typedef KTile<T, BM, kBK> TB;  // h rows of the token block
+  constexpr int BV = C::BV, BM = C::BM, NT = C::NT;
+  constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
+  typedef KTile<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile
+  typedef KTile<T, BM, kBK, NT> TB;  // h rows of the token block
+  typedef KTile<T, BV, DP, NT> TE;   // E tile [BV][DP], swizzled like an operand tile
   constexpr int SB = TA::BYTES + TB::BYTES;
-  constexpr int L = TA::NI + TB::NI;
-  constexpr int FV = BV / 64, FT = BM / 64;  // 32x32 blocks per wave (2 x 2 waves)
+  constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
+  constexpr int FV = WVR / 32, FT = WTR / 32;  // 32x32 blocks per wave
   constexpr int DB = DP / 32;
-  typedef KTile<T, BV, DP> TE;    // E tile [BV][DP], swizzled like an operand tile
   constexpr int EBYTES = TE::BYTES;
   constexpr int BBYTES = BV * 4;
 
@@ -41,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
   const float* const sBias = reinterpret_cast<const float*>(sE + EBYTES);
 
   const int lane = lane_id(), w = wave_id();
-  const int wv = w >> 1, wt = w & 1;
+  const int wv = w / C::WT, wt = w % C::WT;
   const int t = xcd_swizzle(blockIdx.x, p.n_tb * p.n_split);
   const int split = t / p.n_tb, tb = t % p.n_tb;
   const int n0 = tb * BM;
@@ -102,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
         for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
     }
     const char* st = smem + (g % kStages) * SB;
-    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * (BV / 2), wt * (BM / 2), [&] {
+    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * WVR, wt * WTR, [&] {
       if (g + kStages - 1 < total) issue(g + kStages - 1);
     });
     if (kt != nk - 1) continue;
@@ -112,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
       stage_barrier();
     }
 
-    // ---- scores -> running softmax of this wave's half tile
+    // ---- scores -> running softmax of this wave's slice of the tile
     float mx[FT];
 #pragma unroll
     for (int ft = 0; ft < FT; ++ft) mx[ft] = kNegInf;
@@ -120,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float b = sBias[wv * (BV / 2) + fv * 32 + c_row(r, lane)];
+        const float b = sBias[wv * WVR + fv * 32 + c_row(r, lane)];
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
           const float x = sacc[fv][ft][r] * p.scale + b;
@@ -156,6 +173,7 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
     // Score registers 8c..8c+7 of a block are the B operand of one k16 step;
     // they hold vocabulary rows 16c + 8(t/4) + 4(lane/32) + t%4, t = 0..7, so
     // the E^T operand is gathered from LDS with the same row order.
+    const char* sEe = sE + opaque_zero();  // gather base, recomputed per tile
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
@@ -165,8 +183,8 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
         for (int db = 0; db < DB; ++db)
 #pragma unroll
           for (int tt = 0; tt < 8; ++tt) {
-            const int vv = wv * (BV / 2) + fv * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-            av[db][tt] = *reinterpret_cast<const T*>(sE + TE::elem(vv, db * 32 + (lane & 31)));
+            const int vv = wv * WVR + fv * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
+            av[db][tt] = *reinterpret_cast<const T*>(sEe + TE::elem(vv, db * 32 + (lane & 31)));
           }
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
@@ -179,11 +197,11 @@ __global__ __launch_bounds__(kThreads) void fwd_tile_kernel(FwdParams p) {
       }
   }
 
-  // ---- partial (m, l, acc) of this wave's vocabulary half of this split
-  const int part = split * 2 + wv;
+  // ---- partial (m, l, acc) of this wave's vocabulary slice of this split
+  const int part = split * C::WV + wv;
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
-    const int n = n0 + wt * (BM / 2) + ft * 32 + (lane & 31);
+    const int n = n0 + wt * WTR + ft * 32 + (lane & 31);
     if (n < p.N) {
       if (lane < 32) {
         p.part_m[(int64_t)part * p.N + n] = m[ft];
@@ -227,52 +245,44 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   if (d == 0) lse[n] = M + logf(L);
 }
 
-template <class T, int BV, int BM, int DP>
+template <class T, int DP>
 hipError_t launch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
-  const int blocks = plan.n_tb * plan.n_split;
-  timing_begin(kKindFwdTile, stream);
-  fwd_tile_kernel<T, BV, BM, DP><<<blocks, kThreads, 0, stream>>>(p);
-  timing_end(kKindFwdTile, stream);
-  return hipGetLastError();
-}
-
-// Tile shape per (dtype, padded D): the per-wave score block and the acc^T
-// block share the register file; four K-slices of W and h plus the E tile
-// share LDS (160 KB).
-template <class T, int DP>
-struct FwdTile {
-  static constexpr bool wide = sizeof(T) == 2;
-  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
-  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
-};
-
-template <class T, int DP>
-hipError_t dispatch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
   typedef FwdTile<T, DP> C;
   if (plan.BV != C::BV || plan.BM != C::BM) return hipErrorInvalidValue;
-  return launch_tile<T, C::BV, C::BM, DP>(plan, p, stream);
+  const int blocks = plan.n_tb * plan.n_split;
+  timing_begin(kKindFwdTile, stream);
+  fwd_tile_kernel<T, DP><<<blocks, C::NT, 0, stream>>>(p);
+  timing_end(kKindFwdTile, stream);
+  return hipGetLastError();
 }
 
 template <class T>
 hipError_t dispatch_dp(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
   switch (plan.DP) {
-    case 32: return dispatch_tile<T, 32>(plan, p, stream);
-    case 64: return dispatch_tile<T, 64>(plan, p, stream);
-    case 128: return dispatch_tile<T, 128>(plan, p, stream);
+    case 32: return launch_tile<T, 32>(plan, p, stream);
+    case 64: return launch_tile<T, 64>(plan, p, stream);
+    case 128: return launch_tile<T, 128>(plan, p, stream);
     case 256:
-      if constexpr (sizeof(T) == 2) return dispatch_tile<T, 256>(plan, p, stream);
+      if constexpr (sizeof(T) == 2) return launch_tile<T, 256>(plan, p, stream);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
 
+template <class T, int DP>
+void tile_get(int* BV, int* BM, int* WV) {
+  *BV = FwdTile<T, DP>::BV;
+  *BM = FwdTile<T, DP>::BM;
+  *WV = FwdTile<T, DP>::WV;
+}
+
 template <class T>
-void tile_of(int DP, int* BV, int* BM) {
+void tile_of(int DP, int* BV, int* BM, int* WV) {
   switch (DP) {
-    case 32: *BV = FwdTile<T, 32>::BV; *BM = FwdTile<T, 32>::BM; break;
-    case 64: *BV = FwdTile<T, 64>::BV; *BM = FwdTile<T, 64>::BM; break;
-    case 128: *BV = FwdTile<T, 128>::BV; *BM = FwdTile<T, 128>::BM; break;
-    default: *BV = FwdTile<T, 256>::BV; *BM = FwdTile<T, 256>::BM; break;
+    case 32: tile_get<T, 32>(BV, BM, WV); break;
+    case 64: tile_get<T, 64>(BV, BM, WV); break;
+    case 128: tile_get<T, 128>(BV, BM, WV); break;
+    default: tile_get<T, 256>(BV, BM, WV); break;
   }
 }
 
@@ -295,14 +305,14 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   (void)K;
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
-  int BV, BM;
+  int BV, BM, WV;
   size_t tbytes;
   if (dtype == kF32) {
     if (DP > 128) return false;
-    tile_of<float>(DP, &BV, &BM);
+    tile_of<float>(DP, &BV, &BM, &WV);
     tbytes = 4;
   } else if (dtype == kBF16 || dtype == kF16) {
-    tile_of<bf16_t>(DP, &BV, &BM);
+    tile_of<bf16_t>(DP, &BV, &BM, &WV);
     tbytes = 2;
   } else {
     return false;
@@ -313,18 +323,18 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   plan->n_tb = (int)((N + BM - 1) / BM);
   plan->n_vt = (int)((V + BV - 1) / BV);
   plan->V_pad = plan->n_vt * BV;
-  // Enough workgroups to fill 256 CUs several times over, at least two
-  // vocabulary tiles per split.
+  // Enough workgroups (one per CU) to fill 256 CUs several times over, at
+  // least two vocabulary tiles per split.
   int n_split = 1;
   if (plan->n_tb > 0) {
-    const int target = 2048;
+    const int target = 1024;
     n_split = (target + plan->n_tb - 1) / plan->n_tb;
     const int max_split = plan->n_vt / 2 > 1 ? plan->n_vt / 2 : 1;
     if (n_split > max_split) n_split = max_split;
     if (n_split < 1) n_split = 1;
   }
   plan->n_split = n_split;
-  plan->n_part = 2 * n_split;
+  plan->n_part = WV * n_split;
   size_t off = 0;
   plan->off_m = off;
   off += align256((size_t)plan->n_part * N * 4);

@@ -64,7 +64,8 @@ struct BwdPlan {
   int64_t N_pad;         // token stride of the dS stage
   int64_t C;             // vocabulary rows per chunk (multiple of BV)
   int n_chunks;
-  int G;                 // token groups of the dS kernel (dE / db partials)
+  int G;                 // token groups of the dS kernel
+  int n_gpart;           // dE / db partials per chunk
   bool dh_acc;           // dh needs an fp32 accumulator across chunks
   int V_pad;             // vocabulary rows of the packed E / bias
   size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_lsed, off_Ep, off_bias, ws_bytes;
