@@ -149,58 +149,64 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   }
 
   const int nk = (p.K + kBK - 1) / kBK;
-  const int total = (tb_end - tb_begin) * nk;
+  const int n_blocks = tb_end - tb_begin;
   const T* h = static_cast<const T*>(p.h);
   TA ta;
   ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
   TB tw;
   tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
-  auto issue = [&](int gs) {
-    const int kt = gs % nk;
-    if (kt == 0) {
-      const int n0 = (tb_begin + gs / nk) * BM;
+  // issue cursor: the next stage to load (kStages - 1 ahead of the compute)
+  int is_blk = 0, is_kt = 0, is_slot = 0;
+  auto issue_next = [&]() {
+    if (is_blk >= n_blocks) return;
+    if (is_kt == 0) {
+      const int n0 = (tb_begin + is_blk) * BM;
       ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
     }
-    const uint32_t st = lds0 + (gs % kStages) * SB;
-    ta.issue(st, kt * kBK);
-    tw.issue(st + TA::BYTES, kt * kBK);
+    const uint32_t st = lds0 + is_slot * SB;
+    ta.issue(st, is_kt * kBK);
+    tw.issue(st + TA::BYTES, is_kt * kBK);
+    if (++is_kt == nk) {
+      is_kt = 0;
+      ++is_blk;
+    }
+    is_slot = is_slot == kStages - 1 ? 0 : is_slot + 1;
   };
 #pragma unroll
-  for (int gs = 0; gs < kStages - 1; ++gs)
-    if (gs < total) issue(gs);
+  for (int s = 0; s < kStages - 1; ++s) issue_next();
 
   T* stage = static_cast<T*>(p.stage);
   f32x16_t sacc[FT][FV];
-  for (int gs = 0; gs < total; ++gs) {
-    const int kt = gs % nk;
-    const int n0 = (tb_begin + gs / nk) * BM;
-    const int ahead = total - 1 - gs < kStages - 2 ? total - 1 - gs : kStages - 2;
-    wait_stages<L, kStages>(ahead);
-    stage_barrier();
-    if (kt == 0) {
-      // gO, LSE and delta of this token block; every wave has finished the
-      // previous block's epilogue (barrier above)
-      TG tg;
-      tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
-      tg.issue(ldsG, 0);
-      const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
-      if (c < BM / 2) {
-        const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
-        dma_batch1(make_rsrc(p.lsed), off, ldsL + w * 1024);
+  int slot = 0, remaining = n_blocks * nk;
+  for (int blk = 0; blk < n_blocks; ++blk) {
+    const int n0 = (tb_begin + blk) * BM;
+    for (int kt = 0; kt < nk; ++kt) {
+      --remaining;  // stages after this one
+      wait_stages<L, kStages>(remaining);
+      stage_barrier();
+      if (kt == 0) {
+        // gO, LSE and delta of this token block; every wave has finished the
+        // previous block's epilogue (barrier above)
+        TG tg;
+        tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
+        tg.issue(ldsG, 0);
+        const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
+        if (c < BM / 2) {
+          const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
+          dma_batch1(make_rsrc(p.lsed), off, ldsL + w * 1024);
+        }
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+          for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
       }
-#pragma unroll
-      for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-        for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+      const char* st = smem + slot * SB;
+      stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, wt * WTR, wv * WVR, issue_next);
+      slot = slot == kStages - 1 ? 0 : slot + 1;
     }
-    const char* st = smem + (gs % kStages) * SB;
-    stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, wt * WTR, wv * WVR, [&] {
-      if (gs + kStages - 1 < total) issue(gs + kStages - 1);
-    });
-    if (kt != nk - 1) continue;
-    if (nk < kStages || gs < kStages) {
-      // short reduction, or the first block (E / bias were issued before the
-      // stages): make sure every side load has landed
+    if (nk <= kStages) {
+      // short reduction: the side loads (gO / LSE / delta, and E / bias of
+      // the first block) may still be in flight
       wait_vmcnt<0>();
       stage_barrier();
     }

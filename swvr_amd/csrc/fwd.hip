@@ -78,51 +78,57 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   }
 
   const int nk = (p.K + kBK - 1) / kBK;
-  const int total = (vt_end - vt_begin) * nk;
+  const int n_tiles = vt_end - vt_begin;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsE = lds0 + kStages * SB, ldsB = ldsE + EBYTES;
   TA ta;
   ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
   TB tbh;
   tbh.setup(static_cast<const T*>(p.h) + (int64_t)n0 * p.ldh, p.ldh, p.N - n0, p.K);
-  auto issue = [&](int g) {
-    const int kt = g % nk;
-    if (kt == 0) {
-      const int v0 = (vt_begin + g / nk) * BV;
+  // issue cursor: the next stage to load (kStages - 1 ahead of the compute)
+  int is_tile = 0, is_kt = 0, is_slot = 0;
+  auto issue_next = [&]() {
+    if (is_tile >= n_tiles) return;
+    if (is_kt == 0) {
+      const int v0 = (vt_begin + is_tile) * BV;
       ta.rebase(W + (int64_t)v0 * p.ldw, p.V - v0);
     }
-    const uint32_t st = lds0 + (g % kStages) * SB;
-    ta.issue(st, kt * kBK);
-    tbh.issue(st + TA::BYTES, kt * kBK);
+    const uint32_t st = lds0 + is_slot * SB;
+    ta.issue(st, is_kt * kBK);
+    tbh.issue(st + TA::BYTES, is_kt * kBK);
+    if (++is_kt == nk) {
+      is_kt = 0;
+      ++is_tile;
+    }
+    is_slot = is_slot == kStages - 1 ? 0 : is_slot + 1;
   };
 #pragma unroll
-  for (int g = 0; g < kStages - 1; ++g)
-    if (g < total) issue(g);
+  for (int s = 0; s < kStages - 1; ++s) issue_next();
 
   f32x16_t sacc[FV][FT];
-  for (int g = 0; g < total; ++g) {
-    const int kt = g % nk;
-    const int ahead = total - 1 - g < kStages - 2 ? total - 1 - g : kStages - 2;
-    wait_stages<L, kStages>(ahead);
-    stage_barrier();
-    if (kt == 0) {
-      // E and bias tiles of this vocabulary tile; every wave has finished the
-      // previous tile's epilogue (barrier above)
-      const int v0 = (vt_begin + g / nk) * BV;
-      TE te;
-      te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
-      te.issue(ldsE, 0);
-      if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
+  int slot = 0, remaining = n_tiles * nk;
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int v0 = (vt_begin + tile) * BV;
+    for (int kt = 0; kt < nk; ++kt) {
+      --remaining;  // stages after this one
+      wait_stages<L, kStages>(remaining);
+      stage_barrier();
+      if (kt == 0) {
+        // E and bias tiles of this vocabulary tile; every wave has finished
+        // the previous tile's epilogue (barrier above)
+        TE te;
+        te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
+        te.issue(ldsE, 0);
+        if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
 #pragma unroll
-      for (int fv = 0; fv < FV; ++fv)
+        for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
-        for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+          for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+      }
+      const char* st = smem + slot * SB;
+      stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * WVR, wt * WTR, issue_next);
+      slot = slot == kStages - 1 ? 0 : slot + 1;
     }
-    const char* st = smem + (g % kStages) * SB;
-    stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * WVR, wt * WTR, [&] {
-      if (g + kStages - 1 < total) issue(g + kStages - 1);
-    });
-    if (kt != nk - 1) continue;
     if (nk < kStages) {
       // short reduction: the E / bias loads may still be in flight
       wait_vmcnt<0>();
