@@ -148,7 +148,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
     for (int db = 0; db < DB; ++db) deacc[db][fv] = zero16();
   }
 
-  const int nk = (p.K + kBK - 1) / kBK;
+  const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
   const int n_blocks = tb_end - tb_begin;
   const T* h = static_cast<const T*>(p.h);
   TA ta;
@@ -177,33 +177,27 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 
   T* stage = static_cast<T*>(p.stage);
   f32x16_t sacc[FT][FV];
-  int slot = 0, remaining = n_blocks * nk;
+  Ring ring{kStages - 1, n_blocks * nk};  // the first publish_next() moves to stage 0, slot 0
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int n0 = (tb_begin + blk) * BM;
-    for (int kt = 0; kt < nk; ++kt) {
-      --remaining;  // stages after this one
-      wait_stages<L, kStages>(remaining);
-      stage_barrier();
-      if (kt == 0) {
-        // gO, LSE and delta of this token block; every wave has finished the
-        // previous block's epilogue (barrier above)
-        TG tg;
-        tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
-        tg.issue(ldsG, 0);
-        const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
-        if (c < BM / 2) {
-          const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
-          dma_batch1(make_rsrc(p.lsed), off, ldsL + w * 1024);
-        }
-#pragma unroll
-        for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-          for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+    // first stage of the block; every wave has also finished the previous
+    // block's epilogue, so the gO / LSE / delta tiles can be replaced
+    ring.publish_next<L>();
+    {
+      TG tg;
+      tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
+      tg.issue(ldsG, 0);
+      const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
+      if (c < BM / 2) {
+        const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
+        dma_batch1(make_rsrc(p.lsed), off, ldsL + w * 1024);
       }
-      const char* st = smem + slot * SB;
-      stage_mma<T, kBK, FT, FV>(sacc, ta, tw, st, st + TA::BYTES, wt * WTR, wv * WVR, issue_next);
-      slot = slot == kStages - 1 ? 0 : slot + 1;
     }
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+    tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
     if (nk <= kStages) {
       // short reduction: the side loads (gO / LSE / delta, and E / bias of
       // the first block) may still be in flight
@@ -359,23 +353,21 @@ __device__ __forceinline__ void gemm_loop(f32x16_t (&acc)[FM][FN], const TA& ta,
   constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
   const int nk = (k_total + BK - 1) / BK;
   const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int gs) {
-    const uint32_t st = lds0 + (gs % kStages) * SB;
-    ta.issue(st, gs * BK);
-    tb.issue(st + TA::BYTES, gs * BK);
+  int is_k = 0, is_slot = 0;
+  auto issue_next = [&]() {
+    if (is_k >= nk) return;
+    const uint32_t st = lds0 + is_slot * SB;
+    ta.issue(st, is_k * BK);
+    tb.issue(st + TA::BYTES, is_k * BK);
+    ++is_k;
+    is_slot = is_slot == kStages - 1 ? 0 : is_slot + 1;
   };
 #pragma unroll
-  for (int gs = 0; gs < kStages - 1; ++gs)
-    if (gs < nk) issue(gs);
-  for (int gs = 0; gs < nk; ++gs) {
-    const int ahead = nk - 1 - gs < kStages - 2 ? nk - 1 - gs : kStages - 2;
-    wait_stages<L, kStages>(ahead);
-    stage_barrier();
-    const char* st = smem + (gs % kStages) * SB;
-    stage_mma<T, BK, FM, FN>(acc, ta, tb, st, st + TA::BYTES, a_row0, b_row0, [&] {
-      if (gs + kStages - 1 < nk) issue(gs + kStages - 1);
-    });
-  }
+  for (int s = 0; s < kStages - 1; ++s) issue_next();
+  if (nk == 0) return;
+  Ring ring{kStages - 1, nk};
+  ring.publish_next<L>();
+  tile_reduce<T, BK, L>(acc, ta, tb, smem, SB, ring, nk, a_row0, b_row0, issue_next);
 }
 
 // Tile of the gradient GEMMs: GM x GN per workgroup of WM x WN waves

@@ -94,6 +94,7 @@ __device__ __forceinline__ int c_row(int r, int lane) { return (r >> 2) * 8 + (l
 // ----------------------------------------------------------------------------
 typedef int rsrc_t __attribute__((ext_vector_type(4)));  // buffer descriptor (4 SGPRs)
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kStages = 4;   // LDS ring depth of the reduction loop
 constexpr uint32_t kOOB = 0x80000000u;
@@ -378,20 +379,17 @@ __device__ __forceinline__ typename Vec8<T>::type read_op(const RTile<T, R, BK, 
     // of row (lane % 32).
     const int g = (lane >> 4) & 1, a = (lane & 15) >> 2, q = lane & 3;
     const int r = row - (lane & 31) + 16 * g + 4 * q;  // row is this lane's own row (m0 + lane % 32)
-    V8 out;
+    s16x4_t v[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int krow = kb + 4 * h + a;
       const char* p = stage + krow * RT::ROWB + (((r / RT::CE) ^ RT::swz(krow)) * 16) + (r % RT::CE) * 2;
-      const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const short sv = v[t];
-        T e;
-        __builtin_memcpy(&e, &sv, 2);
-        out[4 * h + t] = e;
-      }
+      v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
     }
+    // the two 4-value halves side by side are the 8 values of the operand
+    const s16x8_t both = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    V8 out;
+    __builtin_memcpy(&out, &both, 16);
     return out;
   } else {
     V8 out;
@@ -421,33 +419,97 @@ __global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E
   if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
 }
 
-// acc[FM][FN] += A_stage[a_row0 + ...] * B_stage[b_row0 + ...]^T over the
-// k16 step j of a staged slice.
+// MFMA operands of one k16 step of a wave's FM x FN grid of 32x32 blocks.
+template <class T, int FM, int FN>
+struct StepOps {
+  typename Vec8<T>::type a[FM], b[FN];
+};
+
+// Read the operands of k16 step j of a staged slice (A rows a_row0 + 32 fm +
+// lane % 32, B rows b_row0 + 32 fn + lane % 32).
 template <class T, int FM, int FN, class TA, class TB>
-__device__ __forceinline__ void stage_step(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
-                                           const char* sB, int a_row0, int b_row0, int j) {
-  typedef typename Vec8<T>::type V8;
+__device__ __forceinline__ void load_step(StepOps<T, FM, FN>& o, const TA& ta, const TB& tb, const char* sA,
+                                          const char* sB, int a_row0, int b_row0, int j) {
   const int lr = lane_id() & 31;
-  V8 a[FM], b[FN];
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
+  for (int fm = 0; fm < FM; ++fm) o.a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
 #pragma unroll
-  for (int fn = 0; fn < FN; ++fn) b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+  for (int fn = 0; fn < FN; ++fn) o.b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+}
+
+template <class T, int FM, int FN>
+__device__ __forceinline__ void mma_step(f32x16_t (&acc)[FM][FN], const StepOps<T, FM, FN>& o) {
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], a[fm], b[fn]);
+    for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], o.a[fm], o.b[fn]);
 }
 
-// One stage: the first k16 step, then `between` (the next stage's loads, so
-// that their issue overlaps the matrix work already in flight), then the rest.
-template <class T, int BK, int FM, int FN, class TA, class TB, class F>
-__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* sA,
-                                          const char* sB, int a_row0, int b_row0, F&& between) {
-  stage_step<T, FM, FN>(acc, ta, tb, sA, sB, a_row0, b_row0, 0);
-  between();
+// Position of the compute in the LDS ring: the slot of the current stage and
+// the number of stages after it in the whole walk.
+struct Ring {
+  int slot;
+  int remaining;
+  // Wait until the next stage has landed and publish it to every wave (which
+  // also certifies that every wave has finished reading the stage before it).
+  template <int L>
+  __device__ __forceinline__ void publish_next() {
+    --remaining;
+    wait_stages<L, kStages>(remaining);
+    stage_barrier();
+    slot = slot == kStages - 1 ? 0 : slot + 1;
+  }
+};
+
+// acc += A_slice B_slice^T over the nk stages of one output tile, software-
+// pipelined: the operands of the next k16 step are read from LDS while the
+// current step's matrix work runs, and the wait + barrier that publishes the
+// next stage sits between the last two steps of a stage, so neither the LDS
+// latency nor the barrier leaves the matrix cores idle at a stage boundary.
+// On entry the tile's first stage (ring.slot) is published.  issue_next()
+// issues the next pending stage load into the slot that the stage before the
+// current one used (free once the current stage is published), or nothing
+// when the walk has no more.  On return the ring points at the tile's last
+// stage; the caller publishes the next tile's first stage.
+template <class T, int BK, int L, int FM, int FN, class TA, class TB, class F>
+__device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* smem,
+                                            int sb, Ring& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
+  constexpr int J = BK / 16;
+  StepOps<T, FM, FN> cur, nxt;
+  {
+    const char* sA = smem + ring.slot * sb;
+    load_step(cur, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, 0);
+  }
+  // all stages but the last: the next stage is published between the last
+  // two k16 steps (the last stage is peeled so no branch splits the MFMAs)
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    const char* sA = smem + ring.slot * sb;
+    issue_next();
 #pragma unroll
-  for (int j = 1; j < BK / 16; ++j) stage_step<T, FM, FN>(acc, ta, tb, sA, sB, a_row0, b_row0, j);
+    for (int j = 0; j + 1 < J; ++j) {
+      load_step(nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
+      mma_step(acc, cur);
+      cur = nxt;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the MFMAs above stay ahead of the barrier,
+    ring.template publish_next<L>();
+    __builtin_amdgcn_sched_barrier(0);  // the ones below stay behind it
+    const char* nA = smem + ring.slot * sb;
+    load_step(nxt, ta, tb, nA, nA + TA::BYTES, a_row0, b_row0, 0);
+    mma_step(acc, cur);
+    cur = nxt;
+  }
+  {
+    const char* sA = smem + ring.slot * sb;
+    issue_next();
+#pragma unroll
+    for (int j = 0; j + 1 < J; ++j) {
+      load_step(nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
+      mma_step(acc, cur);
+      cur = nxt;
+    }
+    mma_step(acc, cur);
+  }
 }
 
 // blockIdx -> tile index such that each XCD (blocks are dealt to the 8 XCDs

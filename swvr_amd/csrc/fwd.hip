@@ -77,7 +77,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
     for (int db = 0; db < DB; ++db) oacc[db][ft] = zero16();
   }
 
-  const int nk = (p.K + kBK - 1) / kBK;
+  const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
   const int n_tiles = vt_end - vt_begin;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsE = lds0 + kStages * SB, ldsB = ldsE + EBYTES;
@@ -106,29 +106,23 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   for (int s = 0; s < kStages - 1; ++s) issue_next();
 
   f32x16_t sacc[FV][FT];
-  int slot = 0, remaining = n_tiles * nk;
+  Ring ring{kStages - 1, n_tiles * nk};  // the first publish_next() moves to stage 0, slot 0
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int v0 = (vt_begin + tile) * BV;
-    for (int kt = 0; kt < nk; ++kt) {
-      --remaining;  // stages after this one
-      wait_stages<L, kStages>(remaining);
-      stage_barrier();
-      if (kt == 0) {
-        // E and bias tiles of this vocabulary tile; every wave has finished
-        // the previous tile's epilogue (barrier above)
-        TE te;
-        te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
-        te.issue(ldsE, 0);
-        if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
-#pragma unroll
-        for (int fv = 0; fv < FV; ++fv)
-#pragma unroll
-          for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
-      }
-      const char* st = smem + slot * SB;
-      stage_mma<T, kBK, FV, FT>(sacc, ta, tbh, st, st + TA::BYTES, wv * WVR, wt * WTR, issue_next);
-      slot = slot == kStages - 1 ? 0 : slot + 1;
+    // first stage of the tile; every wave has also finished the previous
+    // tile's epilogue, so the E and bias tiles can be replaced
+    ring.publish_next<L>();
+    {
+      TE te;
+      te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
+      te.issue(ldsE, 0);
+      if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
     }
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+    tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
     if (nk < kStages) {
       // short reduction: the E / bias loads may still be in flight
       wait_vmcnt<0>();

@@ -233,3 +233,26 @@ def test_golden_fixtures_through_hip_fp32(case):
         for red, want in c["mse"].items():
             got = swvr.softmax_readout_mse(*xs[:3], t(c["target"]), xs[3], reduction=red, **kw)
             assert rel_err(got, torch.tensor(want, dtype=f64)) < 1e-5
+
+
+
+def test_zero_hidden_size():
+    # the public API flattens h with reshape(-1, K), which raises for K = 0
+    # exactly as swvr/api.py:36 does
+    h, W, E, b = make(K=0)
+    with pytest.raises(RuntimeError):
+        swvr.softmax_readout(h, W, E, b, chunk_size=8)
+    # the C ABI takes K = 0: every score is the bias, so O = softmax(b) E
+    from swvr_amd import _lib
+    lib = _lib.load()
+    N, V, D = 6, 41, 5
+    Ed, bd = E.detach().contiguous(), b.detach().contiguous()
+    O = torch.empty(N, D, device="cuda")
+    lse = torch.empty(N, device="cuda")
+    ws = torch.empty(lib.swvr_fwd_workspace_size(2, N, 0, V, D), dtype=torch.uint8, device="cuda")
+    _lib.check(lib.swvr_fwd(2, N, 0, V, D, None, 0, None, 0, _lib.ptr(Ed), D, _lib.ptr(bd), 1.0,
+                            _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream_of(O.device)))
+    torch.cuda.synchronize()
+    want = torch.softmax(bd.double(), 0) @ Ed.double()
+    torch.testing.assert_close(O.double(), want.expand_as(O), **TOL)
+    torch.testing.assert_close(lse.double(), torch.logsumexp(bd.double(), 0).expand(N), **TOL)
