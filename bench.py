@@ -3,6 +3,7 @@
     python bench.py                      # headline (config 3), 10 timed steps
     python bench.py --config 2 --steps 20 --warmup 3
     python bench.py --no-cpu             # skip the CPU baseline leg
+    python bench.py --copy-probe-mib 1024  # only a plain device copy (HBM counter calibration)
 
 A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
@@ -85,6 +86,19 @@ def kernel_flops(name, N, K, V, D):
     return 0.0
 
 
+def measured_traffic(config, kernel):
+    """Calibrated HBM bytes per launch of ``kernel`` from the committed counter summary
+    (profiles/readout_traffic.json), or None when it holds no entry for this workload."""
+    path = os.path.join(ROOT, "profiles", "readout_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        e = t["configs"][str(config)][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(e["fetch_kib"] * 1024 * t["fetch_scale"] + e["write_kib"] * 1024 * t["write_scale"])
+
+
 def cpu_baseline(cfg, tokens, chunk, device):
     """Time oracle/chunked.py (the reference's CPU algorithm) fwd+bwd on `tokens` tokens."""
     from oracle import chunked
@@ -106,6 +120,16 @@ def cpu_baseline(cfg, tokens, chunk, device):
                       f"to fp32 BLAS, vocabulary chunk {chunk}) in {dt:.1f} s on {threads} threads"}
 
 
+def copy_probe(mib):
+    """A plain copy of a known size: reads and writes exactly ``mib`` MiB per launch."""
+    src = torch.ones(mib * 2**20 // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_mib": mib, "launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,8 +138,14 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--chunk", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--cpu-tokens", type=int, default=4096)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run only a plain device-to-device copy of this many MiB, 5 times, and exit: "
+                         "its FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc calibrate the HBM traffic counters")
     args = ap.parse_args()
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only (N=1); multi-GPU runs are not part of it"}))
         sys.exit(2)
@@ -202,7 +232,8 @@ def main():
         "we_stream_gbps": round(we_bytes / (ms * 1e-3) / 1e9, 1),
         "kernels": per_kernel,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(args.config, dom)},
         "published_reference_ms": {"A100": {3: 240, 2: 115, 4: 160}.get(args.config),
                                    "H200": {3: 98, 2: 48, 4: 62}.get(args.config)},
     }
