@@ -87,6 +87,7 @@ struct ScoresTile {
   static constexpr int WT = wide && DP == 128 ? 2 : 1;
   static constexpr int WV = wide && DP <= 64 ? 8 : 4;
   static constexpr int NT = 64 * WT * WV;
+  static constexpr int NS = kStages;  // LDS ring depth
 };
 
 // One workgroup: BV vocabulary rows of the chunk x one group of token
@@ -111,8 +112,9 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   constexpr int FT = WTR / 32, FV = WVR / 32;
   constexpr int DB = DP / 32, DK = DP / 16;
 
-  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB + TE::BYTES + TG::BYTES + BV * 4 + 2 * BM * 4];
-  char* const sE = smem + kStages * SB;
+  constexpr int NS = C::NS;
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + TE::BYTES + TG::BYTES + BV * 4 + 2 * BM * 4];
+  char* const sE = smem + NS * SB;
   char* const sG = sE + TE::BYTES;
   float* const sBias = reinterpret_cast<float*>(sG + TG::BYTES);
   float* const sLse = sBias + BV;
@@ -130,7 +132,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 
   // E and bias of the vocabulary tile: once per workgroup, ahead of the stages
   const uint32_t lds0 = lds_addr(smem);
-  const uint32_t ldsE = lds0 + kStages * SB, ldsG = ldsE + TE::BYTES, ldsB = ldsG + TG::BYTES;
+  const uint32_t ldsE = lds0 + NS * SB, ldsG = ldsE + TE::BYTES, ldsB = ldsG + TG::BYTES;
   const uint32_t ldsL = ldsB + BV * 4;
   {
     TE te;
@@ -155,7 +157,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
   TB tw;
   tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
-  // issue cursor: the next stage to load (kStages - 1 ahead of the compute)
+  // issue cursor: the next stage to load (NS - 1 ahead of the compute)
   int is_blk = 0, is_kt = 0, is_slot = 0;
   auto issue_next = [&]() {
     if (is_blk >= n_blocks) return;
@@ -170,19 +172,19 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
       is_kt = 0;
       ++is_blk;
     }
-    is_slot = is_slot == kStages - 1 ? 0 : is_slot + 1;
+    is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
   };
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue_next();
+  for (int s = 0; s < NS - 1; ++s) issue_next();
 
   T* stage = static_cast<T*>(p.stage);
   f32x16_t sacc[FT][FV];
-  Ring ring{kStages - 1, n_blocks * nk};  // the first publish_next() moves to stage 0, slot 0
+  Ring<NS> ring{NS - 1, n_blocks * nk};  // the first publish_next() moves to stage 0, slot 0
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int n0 = (tb_begin + blk) * BM;
     // first stage of the block; every wave has also finished the previous
     // block's epilogue, so the gO / LSE / delta tiles can be replaced
-    ring.publish_next<L>();
+    ring.template publish_next<L>();
     {
       TG tg;
       tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
@@ -198,7 +200,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 #pragma unroll
       for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
     tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
-    if (nk <= kStages) {
+    if (nk <= NS) {
       // short reduction: the side loads (gO / LSE / delta, and E / bias of
       // the first block) may still be in flight
       wait_vmcnt<0>();
@@ -365,7 +367,7 @@ __device__ __forceinline__ void gemm_loop(f32x16_t (&acc)[FM][FN], const TA& ta,
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s) issue_next();
   if (nk == 0) return;
-  Ring ring{kStages - 1, nk};
+  Ring<kStages> ring{kStages - 1, nk};
   ring.publish_next<L>();
   tile_reduce<T, BK, L>(acc, ta, tb, smem, SB, ring, nk, a_row0, b_row0, issue_next);
 }

@@ -96,7 +96,7 @@ typedef int rsrc_t __attribute__((ext_vector_type(4)));  // buffer descriptor (4
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kStages = 4;   // LDS ring depth of the reduction loop
+constexpr int kStages = 4;   // default LDS ring depth of the reduction loop
 constexpr uint32_t kOOB = 0x80000000u;
 
 // Reduction slice per stage: 32 elements (64-byte rows) for bf16 / f16, 16
@@ -223,16 +223,27 @@ __device__ __forceinline__ int opaque_zero() {
   return z;
 }
 
-// Wait until at most `ahead` stages of L loads per thread are outstanding.
+// Wait until the next stage of an NS-deep ring has landed, when `ahead`
+// stages (L loads per thread each) have been issued after it: at most
+// min(ahead, NS - 2) stages may stay outstanding.
 template <int L, int NS>
 __device__ __forceinline__ void wait_stages(int ahead) {
-  static_assert(NS == 4, "ring depth");
-  if (ahead >= 2)
-    wait_vmcnt<2 * L>();
-  else if (ahead == 1)
-    wait_vmcnt<L>();
-  else
+  static_assert(NS >= 2 && NS <= 4, "ring depth");
+  if constexpr (NS == 4) {
+    if (ahead >= 2)
+      wait_vmcnt<2 * L>();
+    else if (ahead == 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+  } else if constexpr (NS == 3) {
+    if (ahead >= 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+  } else {
     wait_vmcnt<0>();
+  }
 }
 
 template <class T, int R, int BK, int NT = kThreads>
@@ -445,9 +456,33 @@ __device__ __forceinline__ void mma_step(f32x16_t (&acc)[FM][FN], const StepOps<
     for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], o.a[fm], o.b[fn]);
 }
 
-// Position of the compute in the LDS ring: the slot of the current stage and
-// the number of stages after it in the whole walk.
+// The matrix work of one k16 step (operands `cur`) fused with the LDS reads of
+// the next step's operands (`nxt`, step j of the slice at sA / sB): the B
+// operands are read first; each A operand is read right after the last MFMA
+// that uses its predecessor, so only one A operand is double-buffered at a
+// time (register budget) while every read still has at least the rest of the
+// step's MFMAs to land.
+template <class T, int FM, int FN, class TA, class TB>
+__device__ __forceinline__ void mma_load_step(f32x16_t (&acc)[FM][FN], const StepOps<T, FM, FN>& cur,
+                                              StepOps<T, FM, FN>& nxt, const TA& ta, const TB& tb, const char* sA,
+                                              const char* sB, int a_row0, int b_row0, int j) {
+  const int lr = lane_id() & 31;
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) nxt.b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], cur.a[fm], cur.b[fn]);
+    nxt.a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Position of the compute in an NS-deep LDS ring: the slot of the current
+// stage and the number of stages after it in the whole walk.
+template <int NS>
 struct Ring {
+  static constexpr int kDepth = NS;
   int slot;
   int remaining;
   // Wait until the next stage has landed and publish it to every wave (which
@@ -455,9 +490,9 @@ struct Ring {
   template <int L>
   __device__ __forceinline__ void publish_next() {
     --remaining;
-    wait_stages<L, kStages>(remaining);
+    wait_stages<L, NS>(remaining);
     stage_barrier();
-    slot = slot == kStages - 1 ? 0 : slot + 1;
+    slot = slot == NS - 1 ? 0 : slot + 1;
   }
 };
 
@@ -471,9 +506,9 @@ struct Ring {
 // current one used (free once the current stage is published), or nothing
 // when the walk has no more.  On return the ring points at the tile's last
 // stage; the caller publishes the next tile's first stage.
-template <class T, int BK, int L, int FM, int FN, class TA, class TB, class F>
+template <class T, int BK, int L, int FM, int FN, class TA, class TB, class R, class F>
 __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* smem,
-                                            int sb, Ring& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
+                                            int sb, R& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
   constexpr int J = BK / 16;
   StepOps<T, FM, FN> cur, nxt;
   {
@@ -487,16 +522,14 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
     issue_next();
 #pragma unroll
     for (int j = 0; j + 1 < J; ++j) {
-      load_step(nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
-      mma_step(acc, cur);
+      mma_load_step(acc, cur, nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
       cur = nxt;
     }
     __builtin_amdgcn_sched_barrier(0);  // the MFMAs above stay ahead of the barrier,
     ring.template publish_next<L>();
     __builtin_amdgcn_sched_barrier(0);  // the ones below stay behind it
     const char* nA = smem + ring.slot * sb;
-    load_step(nxt, ta, tb, nA, nA + TA::BYTES, a_row0, b_row0, 0);
-    mma_step(acc, cur);
+    mma_load_step(acc, cur, nxt, ta, tb, nA, nA + TA::BYTES, a_row0, b_row0, 0);
     cur = nxt;
   }
   {
@@ -504,8 +537,7 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
     issue_next();
 #pragma unroll
     for (int j = 0; j + 1 < J; ++j) {
-      load_step(nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
-      mma_step(acc, cur);
+      mma_load_step(acc, cur, nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
       cur = nxt;
     }
     mma_step(acc, cur);

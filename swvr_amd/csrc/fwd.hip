@@ -24,17 +24,63 @@ namespace {
 
 // Tile shape per (dtype, padded D): BV vocabulary rows x BM tokens per
 // workgroup of WV x WT waves (two waves per SIMD for bf16 / f16); the
-// per-wave score block and acc^T block share the register file, four
-// K-slices of W and h plus the E tile share LDS (160 KB).
+// per-wave score block and acc^T block share the register file, NS K-slices
+// of W and h plus the E^T tile and the bias share LDS (160 KB).  For the
+// narrow embeddings (DP <= 64) each wave owns 128 vocabulary rows x 64
+// tokens: 0.75 operand reads per MFMA.
 template <class T, int DP>
 struct FwdTile {
   static constexpr bool wide = sizeof(T) == 2;
+  static constexpr bool narrow = wide && DP <= 64;
   static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
-  static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
-  static constexpr int WV = wide ? (DP == 128 ? 2 : 4) : 2;
-  static constexpr int WT = wide ? (DP == 128 ? 4 : 2) : 2;
+  static constexpr int BM = narrow ? 256 : wide ? (DP <= 128 ? 128 : 64) : 64;
+  static constexpr int WV = narrow ? 2 : wide ? (DP == 128 ? 2 : 4) : 2;
+  static constexpr int WT = narrow ? 4 : wide ? (DP == 128 ? 4 : 2) : 2;
   static constexpr int NT = 64 * WV * WT;
+  static constexpr int NS = narrow ? 3 : kStages;  // LDS ring depth
 };
+
+// Order of the 8 vocabulary rows an E^T operand (lane half `hi`, k16 step c
+// of a 32-row block) pairs with score registers 8c..8c+7: rows
+// 16c + 8(t/4) + 4hi + t%4 for t = 0..7.  The forward packs E^T with each
+// such group of 8 contiguous, so one operand is one 16-byte LDS read.
+__host__ __device__ __forceinline__ int pe_row(int p) {
+  const int blk = p >> 5, g = (p >> 3) & 3, i = p & 7;
+  const int c = g >> 1, hi = g & 1;
+  return blk * 32 + 16 * c + 8 * (i >> 2) + 4 * hi + (i & 3);
+}
+
+// Vocabulary operands of the forward, packed once per call: E^T per
+// vocabulary tile as [n_vt][DP][BV] (compute dtype; column p of tile vt is
+// row vt * BV + pe_row(p) of E; zero past D and V) and the bias as fp32
+// [V_pad] (-inf past V: padding rows drop out of the softmax).
+template <class T>
+__global__ __launch_bounds__(256) void pack_et_kernel(const T* __restrict__ E, int64_t lde,
+                                                      const float* __restrict__ bias, int V, int D, int V_pad,
+                                                      int DP, int BV, T* __restrict__ Et, float* __restrict__ biasp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < (int64_t)V_pad * DP) {
+    const int64_t tile = e / ((int64_t)DP * BV);
+    const int rem = (int)(e - tile * DP * BV);
+    const int d = rem / BV, p = rem % BV;
+    const int64_t v = tile * BV + pe_row(p);
+    Et[e] = (v < V && d < D) ? E[v * lde + d] : (T)0.f;
+  }
+  if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
+}
+
+// Workgroup index -> (row, col) of an R x Q tile grid such that the 32
+// workgroups an XCD runs together cover a 4 x 8 patch (4 rows, 8 columns):
+// blocks go to the XCDs round-robin, xcd_swizzle gives each XCD a contiguous
+// range of the tile order, and the order walks 4-row column strips.
+__device__ __forceinline__ void grouped_tile(int b, int R, int Q, int* row, int* col) {
+  constexpr int G = 4;
+  const int t = xcd_swizzle(b, R * Q);
+  const int group = t / (G * Q), first = group * G;
+  const int gsize = min(R - first, G);
+  *row = first + (t % (G * Q)) % gsize;
+  *col = (t % (G * Q)) / gsize;
+}
 
 template <class T, int DP>
 __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParams p) {
@@ -45,7 +91,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
   typedef KTile<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile
   typedef KTile<T, BM, kBK, NT> TB;  // h rows of the token block
-  typedef KTile<T, BV, DP, NT> TE;   // E tile [BV][DP], swizzled like an operand tile
+  typedef KTile<T, DP, BV, NT> TE;   // E^T tile [DP][BV] in pe_row order, swizzled like an operand tile
   constexpr int SB = TA::BYTES + TB::BYTES;
   constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
   constexpr int FV = WVR / 32, FT = WTR / 32;  // 32x32 blocks per wave
@@ -53,14 +99,15 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   constexpr int EBYTES = TE::BYTES;
   constexpr int BBYTES = BV * 4;
 
-  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB + EBYTES + BBYTES];
-  char* const sE = smem + kStages * SB;
+  constexpr int NS = C::NS;
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + EBYTES + BBYTES];
+  char* const sE = smem + NS * SB;
   const float* const sBias = reinterpret_cast<const float*>(sE + EBYTES);
 
   const int lane = lane_id(), w = wave_id();
   const int wv = w / C::WT, wt = w % C::WT;
-  const int t = xcd_swizzle(blockIdx.x, p.n_tb * p.n_split);
-  const int split = t / p.n_tb, tb = t % p.n_tb;
+  int split, tb;
+  grouped_tile(blockIdx.x, p.n_split, p.n_tb, &split, &tb);
   const int n0 = tb * BM;
   const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
   const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
@@ -80,12 +127,12 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
   const int n_tiles = vt_end - vt_begin;
   const uint32_t lds0 = lds_addr(smem);
-  const uint32_t ldsE = lds0 + kStages * SB, ldsB = ldsE + EBYTES;
+  const uint32_t ldsE = lds0 + NS * SB, ldsB = ldsE + EBYTES;
   TA ta;
   ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
   TB tbh;
   tbh.setup(static_cast<const T*>(p.h) + (int64_t)n0 * p.ldh, p.ldh, p.N - n0, p.K);
-  // issue cursor: the next stage to load (kStages - 1 ahead of the compute)
+  // issue cursor: the next stage to load (NS - 1 ahead of the compute)
   int is_tile = 0, is_kt = 0, is_slot = 0;
   auto issue_next = [&]() {
     if (is_tile >= n_tiles) return;
@@ -100,21 +147,21 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
       is_kt = 0;
       ++is_tile;
     }
-    is_slot = is_slot == kStages - 1 ? 0 : is_slot + 1;
+    is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
   };
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue_next();
+  for (int s = 0; s < NS - 1; ++s) issue_next();
 
   f32x16_t sacc[FV][FT];
-  Ring ring{kStages - 1, n_tiles * nk};  // the first publish_next() moves to stage 0, slot 0
+  Ring<NS> ring{NS - 1, n_tiles * nk};  // the first publish_next() moves to stage 0, slot 0
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int v0 = (vt_begin + tile) * BV;
     // first stage of the tile; every wave has also finished the previous
     // tile's epilogue, so the E and bias tiles can be replaced
-    ring.publish_next<L>();
+    ring.template publish_next<L>();
     {
       TE te;
-      te.setup(Ep + (int64_t)v0 * DP, DP, BV, DP);
+      te.setup(Ep + (int64_t)v0 * DP, BV, DP, BV);
       te.issue(ldsE, 0);
       if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
     }
@@ -123,7 +170,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
     tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
-    if (nk < kStages) {
+    if (nk < NS) {
       // short reduction: the E / bias loads may still be in flight
       wait_vmcnt<0>();
       stage_barrier();
@@ -136,14 +183,18 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float b = sBias[wv * WVR + fv * 32 + c_row(r, lane)];
+      for (int g = 0; g < 4; ++g) {
+        // registers 4g..4g+3 hold rows 8g + 4(lane/32) + 0..3 of the block
+        const float4 b4 = *reinterpret_cast<const float4*>(sBias + wv * WVR + fv * 32 + 8 * g + (lane >> 5) * 4);
+        const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-        for (int ft = 0; ft < FT; ++ft) {
-          const float x = sacc[fv][ft][r] * p.scale + b;
-          sacc[fv][ft][r] = x;
-          mx[ft] = fmaxf(mx[ft], x);
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int ft = 0; ft < FT; ++ft) {
+            const float x = sacc[fv][ft][4 * g + i] * p.scale + bb[i];
+            sacc[fv][ft][4 * g + i] = x;
+            mx[ft] = fmaxf(mx[ft], x);
+          }
       }
 #pragma unroll
     for (int ft = 0; ft < FT; ++ft) {
@@ -171,21 +222,28 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
 
     // ---- acc^T[d][token] += E^T[d][v] P^T[v][token]
     // Score registers 8c..8c+7 of a block are the B operand of one k16 step;
-    // they hold vocabulary rows 16c + 8(t/4) + 4(lane/32) + t%4, t = 0..7, so
-    // the E^T operand is gathered from LDS with the same row order.
-    const char* sEe = sE + opaque_zero();  // gather base, recomputed per tile
+    // they hold vocabulary rows 16c + 8(t/4) + 4(lane/32) + t%4, t = 0..7,
+    // which the packed E^T tile stores contiguously (pe_row): one read per
+    // operand.
+    const char* sEe = sE + opaque_zero();  // read base, recomputed per tile
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         V8 av[DB];
+        const int p0 = wv * WVR + fv * 32 + 8 * (2 * c + (lane >> 5));
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int tt = 0; tt < 8; ++tt) {
-            const int vv = wv * WVR + fv * 32 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-            av[db][tt] = *reinterpret_cast<const T*>(sEe + TE::elem(vv, db * 32 + (lane & 31)));
+        for (int db = 0; db < DB; ++db) {
+          const int d = db * 32 + (lane & 31);
+          if constexpr (sizeof(T) == 2) {
+            av[db] = *reinterpret_cast<const V8*>(sEe + TE::elem(d, p0));
+          } else {
+            const float4 lo = *reinterpret_cast<const float4*>(sEe + TE::elem(d, p0));
+            const float4 hi = *reinterpret_cast<const float4*>(sEe + TE::elem(d, p0 + 4));
+            av[db][0] = lo.x; av[db][1] = lo.y; av[db][2] = lo.z; av[db][3] = lo.w;
+            av[db][4] = hi.x; av[db][5] = hi.y; av[db][6] = hi.z; av[db][7] = hi.w;
           }
+        }
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
           V8 bv;
@@ -292,8 +350,8 @@ template <class T>
 hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   const int64_t n = (int64_t)plan.V_pad * plan.DP;
   timing_begin(kKindPack, stream);
-  pack_vocab_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
-      static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP,
+  pack_et_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
+      static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
       const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
   timing_end(kKindPack, stream);
   return hipGetLastError();

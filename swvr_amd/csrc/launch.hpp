@@ -38,7 +38,7 @@ struct FwdParams {
   float* part_m;       // [n_part][N]
   float* part_l;       // [n_part][N]
   float* part_acc;     // [n_part][DP][N]
-  const void* Ep;      // packed E [V_pad][DP], compute dtype
+  const void* Ep;      // packed E^T tiles [n_vt][DP][BV], compute dtype
   const float* biasp;  // packed bias [V_pad], -inf past V
 };
 
