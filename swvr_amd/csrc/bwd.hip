@@ -30,17 +30,27 @@ __device__ __forceinline__ void store_as(void* base, int64_t idx, int dtype, flo
 // ---------------------------------------------------------------- token-side packing
 // delta = rowsum(O * gO) - gLSE (swvr/chunked.py:113-114), and the token-side
 // operands of the scores kernel packed over N_pad rows: gO rounded to the
-// compute dtype (swvr/chunked.py:115) as [N_pad][DP] (zero padded), and
+// compute dtype (swvr/chunked.py:115) as [N_pad][DP] (zero padded), the same
+// values transposed per token block as [N_pad / BM][DP][BM] with the tokens
+// of a block in pe_row order (the A operand of dE^T = gO^T P), and
 // [lse | delta] as 2 x N_pad floats (lse = +inf on padding rows: P = 0 there).
 template <class T>
 __global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__ O, const float* __restrict__ gO,
                                                        const float* __restrict__ lse,
                                                        const float* __restrict__ glse, int N, int D, int N_pad,
-                                                       int DP, T* __restrict__ gOp, float* __restrict__ lsed) {
+                                                       int DP, int BM, T* __restrict__ gOp, T* __restrict__ gOt,
+                                                       float* __restrict__ lsed) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (int64_t)N_pad * DP) return;
   const int n = (int)(e / DP), d = (int)(e % DP);
   gOp[e] = (n < N && d < D) ? from_float<T>(gO[(int64_t)n * D + d]) : (T)0.f;
+  {
+    const int64_t blk = e / ((int64_t)DP * BM);
+    const int rem = (int)(e - blk * DP * BM);
+    const int dt = rem / BM, q = rem % BM;
+    const int64_t nt = blk * BM + pe_row(q);
+    gOt[e] = (nt < N && dt < D) ? from_float<T>(gO[nt * D + dt]) : (T)0.f;
+  }
   if (d == 0) {
     float s = 0.f;
     if (n < N) {
@@ -63,6 +73,7 @@ struct ScoresParams {
   float scale;
   int N, K;
   const void* gOp;      // packed gO [N_pad][DP]
+  const void* gOt;      // packed gO^T per token block [N_pad / BM][DP][BM], pe_row order
   const float* lsed;    // [lse | delta], 2 x N_pad
   int N_pad;
   int v0, cv;           // chunk start and rows
@@ -85,9 +96,13 @@ struct ScoresTile {
   static constexpr int BM = wide ? (DP <= 128 ? 128 : 64) : 64;
   static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
   static constexpr int WT = wide && DP == 128 ? 2 : 1;
-  static constexpr int WV = wide && DP <= 64 ? 8 : 4;
+  static constexpr int WV = 4;
   static constexpr int NT = 64 * WT * WV;
-  static constexpr int NS = kStages;  // LDS ring depth
+  // LDS: the K-slice ring plus E [BV][DP], gO [BM][DP], gO^T [DP][BM], bias
+  // and LSE / delta; the ring is as deep as the 160 KB allow (at most 4).
+  static constexpr int SIDE = (BV + 2 * BM) * DP * (int)sizeof(T) + BV * 4 + 2 * BM * 4;
+  static constexpr int SB = (BM + BV) * 64;
+  static constexpr int NS = SIDE + 4 * SB <= 160 * 1024 ? 4 : SIDE + 3 * SB <= 160 * 1024 ? 3 : 2;
 };
 
 // One workgroup: BV vocabulary rows of the chunk x one group of token
@@ -107,16 +122,19 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
   typedef KTile<T, BV, DP, NT> TE;   // E tile
   typedef KTile<T, BM, DP, NT> TG;   // gO tile
+  typedef KTile<T, DP, BM, NT> TGT;  // gO^T tile, tokens in pe_row order
   constexpr int SB = TA::BYTES + TB::BYTES;
+  static_assert(SB == C::SB, "stage size");
   constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
   constexpr int FT = WTR / 32, FV = WVR / 32;
   constexpr int DB = DP / 32, DK = DP / 16;
 
   constexpr int NS = C::NS;
-  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + TE::BYTES + TG::BYTES + BV * 4 + 2 * BM * 4];
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + TE::BYTES + TG::BYTES + TGT::BYTES + BV * 4 + 2 * BM * 4];
   char* const sE = smem + NS * SB;
   char* const sG = sE + TE::BYTES;
-  float* const sBias = reinterpret_cast<float*>(sG + TG::BYTES);
+  char* const sGt = sG + TG::BYTES;
+  float* const sBias = reinterpret_cast<float*>(sGt + TGT::BYTES);
   float* const sLse = sBias + BV;
   float* const sDelta = sLse + BM;
 
@@ -132,7 +150,8 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 
   // E and bias of the vocabulary tile: once per workgroup, ahead of the stages
   const uint32_t lds0 = lds_addr(smem);
-  const uint32_t ldsE = lds0 + NS * SB, ldsG = ldsE + TE::BYTES, ldsB = ldsG + TG::BYTES;
+  const uint32_t ldsE = lds0 + NS * SB, ldsG = ldsE + TE::BYTES, ldsGt = ldsG + TG::BYTES;
+  const uint32_t ldsB = ldsGt + TGT::BYTES;
   const uint32_t ldsL = ldsB + BV * 4;
   {
     TE te;
@@ -189,6 +208,9 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
       TG tg;
       tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP);
       tg.issue(ldsG, 0);
+      TGT tgt;
+      tgt.setup(static_cast<const T*>(p.gOt) + (int64_t)n0 * DP, BM, DP, BM);
+      tgt.issue(ldsGt, 0);
       const int c = threadIdx.x;  // BM/4 chunks of LSE, then BM/4 of delta
       if (c < BM / 2) {
         const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
@@ -218,6 +240,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
         // LDS bases recomputed per block (see opaque_zero)
         const int oz = opaque_zero();
         const char* sGe = sG + oz;
+        const char* sGte = sGt + oz;
         const char* sEe = sE + oz;
         const float* sLe = sLse + oz;
         const float* sDe = sDelta + oz;
@@ -229,14 +252,22 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
           mfma_k16(dp, read_op(tgl, sGe, tr0 + (lane & 31), kd), read_op(tel, sEe, vl, kd));
         float dbs = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tl = tr0 + c_row(r, lane);
-          const float x = sacc[ft][fv][r] * p.scale + bvv;
-          const float pv = fast_exp(x - sLe[tl]);
-          const float ds = pv * (dp[r] - sDe[tl]);
-          dbs += ds;
-          sacc[ft][fv][r] = pv;
-          dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
+        for (int g4 = 0; g4 < 4; ++g4) {
+          // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
+          const int tl = tr0 + 8 * g4 + (lane >> 5) * 4;
+          const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
+          const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g4 + i;
+            const float x = sacc[ft][fv][r] * p.scale + bvv;
+            const float pv = fast_exp(x - lv[i]);
+            const float ds = pv * (dp[r] - dv[i]);
+            dbs += ds;
+            sacc[ft][fv][r] = pv;
+            dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
+          }
         }
         dbacc[fv] += dbs;
         if (p.need_stage) {
@@ -258,19 +289,25 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
         }
         if (p.need_dE) {
           // dE^T[d][v] += gO^T[d][tok] P[tok][v]; registers 8c..8c+7 hold
-          // tokens 16c + 8(t/4) + 4(lane/32) + t%4, gathered likewise from sG
+          // tokens 16c + 8(t/4) + 4(lane/32) + t%4, stored contiguously in
+          // the gO^T tile (pe_row order): one read per operand
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             V8 bv;
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[ft][fv][8 * c + tt]);
+            const int p0 = tr0 + 8 * (2 * c + (lane >> 5));
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
+              const int d = db * 32 + (lane & 31);
               V8 av;
-#pragma unroll
-              for (int tt = 0; tt < 8; ++tt) {
-                const int tl = tr0 + 16 * c + 8 * (tt >> 2) + (lane >> 5) * 4 + (tt & 3);
-                av[tt] = *reinterpret_cast<const T*>(sGe + TG::elem(tl, db * 32 + (lane & 31)));
+              if constexpr (sizeof(T) == 2) {
+                av = *reinterpret_cast<const V8*>(sGte + TGT::elem(d, p0));
+              } else {
+                const float4 lo = *reinterpret_cast<const float4*>(sGte + TGT::elem(d, p0));
+                const float4 hi = *reinterpret_cast<const float4*>(sGte + TGT::elem(d, p0 + 4));
+                av[0] = lo.x; av[1] = lo.y; av[2] = lo.z; av[3] = lo.w;
+                av[4] = hi.x; av[5] = hi.y; av[6] = hi.z; av[7] = hi.w;
               }
               mfma_k16(deacc[db][fv], av, bv);
             }
@@ -540,6 +577,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   float* part_db = reinterpret_cast<float*>(ws + plan.off_pb);
   float* dh_acc = plan.dh_acc ? reinterpret_cast<float*>(ws + plan.off_dh) : nullptr;
   T* gOp = reinterpret_cast<T*>(ws + plan.off_gO);
+  T* gOt = reinterpret_cast<T*>(ws + plan.off_gOt);
   float* lsed = reinterpret_cast<float*>(ws + plan.off_lsed);
   T* Ep = reinterpret_cast<T*>(ws + plan.off_Ep);
   float* biasp = reinterpret_cast<float*>(ws + plan.off_bias);
@@ -548,7 +586,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     const int64_t n = (int64_t)plan.N_pad * plan.DP;
     timing_begin(kKindBwdDelta, stream);
     bwd_pack_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(p.O, p.gO, p.lse, p.glse, p.N, p.D,
-                                                                   (int)plan.N_pad, plan.DP, gOp, lsed);
+                                                                   (int)plan.N_pad, plan.DP, plan.BM, gOp, gOt,
+                                                                   lsed);
     timing_end(kKindBwdDelta, stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int64_t nv = (int64_t)plan.V_pad * plan.DP;
@@ -574,6 +613,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.N = p.N;
     sp.K = p.K;
     sp.gOp = gOp;
+    sp.gOt = gOt;
     sp.lsed = lsed;
     sp.N_pad = (int)plan.N_pad;
     sp.v0 = v0;
@@ -700,6 +740,8 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->off_dh = off;
   if (plan->dh_acc) off += align256((size_t)N * K * 4);
   plan->off_gO = off;
+  off += align256((size_t)plan->N_pad * DP * tb);
+  plan->off_gOt = off;
   off += align256((size_t)plan->N_pad * DP * tb);
   plan->off_lsed = off;
   off += align256((size_t)plan->N_pad * 2 * 4);

@@ -72,6 +72,18 @@ template <class T> __device__ __forceinline__ float to_float(T x) { return (floa
 // Row of the C/D block held by register r of this lane.
 __device__ __forceinline__ int c_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
+// A product whose B operand is taken from another product's C/D registers
+// 8c..8c+7 (lane half hi) reduces over the rows 16c + 8(t/4) + 4hi + t%4,
+// t = 0..7, of a 32-row block.  Operand tiles that feed such products store
+// each group of 8 rows contiguously: position p of a packed tile holds row
+// pe_row(p), so an operand is one 16-byte (two for fp32) LDS read at
+// position 32 blk + 8 (2c + hi).
+__host__ __device__ __forceinline__ int pe_row(int p) {
+  const int blk = p >> 5, g = (p >> 3) & 3, i = p & 7;
+  const int c = g >> 1, hi = g & 1;
+  return blk * 32 + 16 * c + 8 * (i >> 2) + 4 * hi + (i & 3);
+}
+
 // ----------------------------------------------------------------------------
 // Direct-to-LDS operand pipeline.
 //

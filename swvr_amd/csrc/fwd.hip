@@ -40,16 +40,6 @@ struct FwdTile {
   static constexpr int NS = narrow ? 3 : kStages;  // LDS ring depth
 };
 
-// Order of the 8 vocabulary rows an E^T operand (lane half `hi`, k16 step c
-// of a 32-row block) pairs with score registers 8c..8c+7: rows
-// 16c + 8(t/4) + 4hi + t%4 for t = 0..7.  The forward packs E^T with each
-// such group of 8 contiguous, so one operand is one 16-byte LDS read.
-__host__ __device__ __forceinline__ int pe_row(int p) {
-  const int blk = p >> 5, g = (p >> 3) & 3, i = p & 7;
-  const int c = g >> 1, hi = g & 1;
-  return blk * 32 + 16 * c + 8 * (i >> 2) + 4 * hi + (i & 3);
-}
-
 // Vocabulary operands of the forward, packed once per call: E^T per
 // vocabulary tile as [n_vt][DP][BV] (compute dtype; column p of tile vt is
 // row vt * BV + pe_row(p) of E; zero past D and V) and the bias as fp32

@@ -68,7 +68,7 @@ struct BwdPlan {
   int n_gpart;           // dE / db partials per chunk
   bool dh_acc;           // dh needs an fp32 accumulator across chunks
   int V_pad;             // vocabulary rows of the packed E / bias
-  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_lsed, off_Ep, off_bias, ws_bytes;
+  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, ws_bytes;
 };
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
