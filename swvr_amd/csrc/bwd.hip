@@ -362,26 +362,35 @@ struct GemmParams {
 
 // Write a GEMM accumulator tile: out[(row_off + row) * ld + col] = acc (+ prev[...]),
 // rows < rows, cols < ld.  prev (fp32, may alias out) is added when non-null.
+// prev may alias out (the running fp32 dh): the previous values of a row of
+// blocks are all loaded before any of them is overwritten, so the loads do not
+// wait for one store after another.
 template <int FM, int FN, class OutT>
 __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], OutT* out, const float* prev,
                                            int64_t row_off, int rows, int row0, int col0, int ld) {
   const int lane = lane_id();
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm)
+  for (int fm = 0; fm < FM; ++fm) {
+    float pv[FN][16];
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
       const int col = col0 + fn * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = row0 + fm * 32 + c_row(r, lane);
-        if (row < rows && col < ld) {
-          const int64_t idx = (row_off + row) * ld + col;
-          float v = acc[fm][fn][r];
-          if (prev) v += prev[idx];
-          out[idx] = (OutT)v;
-        }
+        pv[fn][r] = (prev && row < rows && col < ld) ? prev[(row_off + row) * ld + col] : 0.f;
       }
     }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int col = col0 + fn * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + fm * 32 + c_row(r, lane);
+        if (row < rows && col < ld) out[(row_off + row) * ld + col] = (OutT)(acc[fm][fn][r] + pv[fn][r]);
+      }
+    }
+  }
 }
 
 // Single-tile pipelined reduction: acc += A[.., 0:k_total] B[.., 0:k_total]^T.
