@@ -339,6 +339,248 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   }
 }
 
+// ---------------------------------------------------------------- scores, narrow embeddings
+// bf16 / f16 with DP <= 64: 256 tokens x 256 vocabulary rows per workgroup of
+// 8 waves (2 token halves x 4 vocabulary quarters, 128 x 64 per wave, 0.75
+// operand reads per MFMA).  The LDS is a 4-slot ring of 32 KB; per token block
+// it carries the nk K-slices of h and W, then three side tiles for the
+// epilogue: E [BV][DP], gO [BM][DP] and gO^T [DP][BM] (tokens in pe_row
+// order).  The side slots stay pinned through the epilogue; the next block's
+// slices then catch up.  The bias sits in registers, LSE / delta in a
+// double-buffered LDS strip.
+template <class T, int DP>
+struct ScoresRingTile {
+  static constexpr int BM = 256, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
+};
+
+template <class T, int DP>
+__global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
+  typedef ScoresRingTile<T, DP> C;
+  typedef typename Vec8<T>::type V8;
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int BM = C::BM, BV = C::BV, NT = C::NT, NS = C::NS;
+  constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
+  typedef KTile<T, BM, kBK, NT> TA;  // h rows of the token block
+  typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
+  typedef KTile<T, BV, DP, NT> TE;   // E tile
+  typedef KTile<T, BM, DP, NT> TG;   // gO tile
+  typedef KTile<T, DP, BM, NT> TGT;  // gO^T tile, tokens in pe_row order
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;  // loads per thread per stage, side stages padded to it
+  static_assert(!TA::PARTIAL && !TB::PARTIAL && !TE::PARTIAL && !TG::PARTIAL && !TGT::PARTIAL, "whole loads");
+  static_assert(TE::NI <= L && TG::NI <= L && TGT::NI <= L, "side tiles fit a slot");
+  constexpr int FT = WTR / 32, FV = WVR / 32;
+  constexpr int DB = DP / 32, DK = DP / 16;
+
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4];
+  float* const sLD = reinterpret_cast<float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
+
+  const int lane = lane_id(), w = wave_id();
+  const int wt = w / C::WV, wv = w % C::WV;
+  int vt, g;
+  grouped_tile(blockIdx.x, p.n_vtc, p.G, &vt, &g);
+  const int vl0 = vt * BV;      // first chunk-local row of this tile
+  const int vg0 = p.v0 + vl0;   // its global row
+  const int rows = p.cv - vl0;  // valid rows of this tile (may exceed BV)
+  const int tb_begin = (int)((int64_t)g * p.n_tb / p.G);
+  const int tb_end = (int)((int64_t)(g + 1) * p.n_tb / p.G);
+  const int n_blocks = tb_end - tb_begin;
+
+  f32x16_t deacc[DB][FV];
+  float dbacc[FV], bvv[FV];
+#pragma unroll
+  for (int fv = 0; fv < FV; ++fv) {
+    dbacc[fv] = 0.f;
+    const int vl = wv * WVR + fv * 32 + (lane & 31);
+    bvv[fv] = vl < rows ? p.biasp[vg0 + vl] : kNegInf;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) deacc[db][fv] = zero16();
+  }
+
+  const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
+  const int per_blk = nk + 3;
+  const int total = n_blocks * per_blk;
+  const T* h = static_cast<const T*>(p.h);
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsL = lds0 + NS * SB;
+  TA ta;
+  ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
+  TB tw;
+  tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
+  const rsrc_t r_none = make_rsrc(nullptr);
+  // issue cursor over the walk: stage `issued` is (block is_blk, sub-stage
+  // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk, nk+1, nk+2
+  // the E, gO and gO^T tiles
+  int issued = 0, is_blk = 0, is_sub = 0, is_slot = 0;
+  auto pad = [&](int n_real, uint32_t st) {  // zero-filling loads up to L per thread
+#pragma unroll
+    for (int i = n_real; i < L; ++i) dma_batch1(r_none, kOOB, st + i * NT * 16 + w * 1024);
+  };
+  auto issue_next = [&]() {
+    if (issued >= total) return;
+    const uint32_t st = lds0 + is_slot * SB;
+    const int n0 = (tb_begin + is_blk) * BM;
+    if (is_sub < nk) {
+      if (is_sub == 0) {
+        ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
+        // LSE and delta of the block into strip (block & 1), ahead of its slices
+        const int c = threadIdx.x;
+        if (c < BM / 2) {
+          const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
+          dma_batch1(make_rsrc(p.lsed), off, ldsL + (is_blk & 1) * (2 * BM * 4) + w * 1024);
+        }
+      }
+      ta.issue(st, is_sub * kBK);
+      tw.issue(st + TA::BYTES, is_sub * kBK);
+    } else if (is_sub == nk) {
+      TE te;
+      // an opaque thread index: the load offsets are computed here, once per
+      // block, instead of being hoisted out of the walk (registers)
+      te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP, (int)threadIdx.x + opaque_zero());
+      te.issue(st, 0);
+      pad(TE::NI, st);
+    } else if (is_sub == nk + 1) {
+      TG tg;
+      tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP, (int)threadIdx.x + opaque_zero());
+      tg.issue(st, 0);
+      pad(TG::NI, st);
+    } else {
+      TGT tgt;
+      tgt.setup(static_cast<const T*>(p.gOt) + (int64_t)n0 * DP, BM, DP, BM, (int)threadIdx.x + opaque_zero());
+      tgt.issue(st, 0);
+      pad(TGT::NI, st);
+    }
+    ++issued;
+    if (++is_sub == per_blk) {
+      is_sub = 0;
+      ++is_blk;
+    }
+    is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue_next();
+
+  T* stage = static_cast<T*>(p.stage);
+  f32x16_t sacc[FT][FV];
+  CountedRing<NS> ring{NS - 1, -1, &issued};
+  ring.template publish_next<L>();  // block 0, slice 0
+  for (int blk = 0; blk < n_blocks; ++blk) {
+    const int n0 = (tb_begin + blk) * BM;
+    if (blk > 0) {
+      // slice 0 of this block: every wave has finished the previous epilogue,
+      // so its three side slots are free: catch up to NS - 1 stages ahead
+      ring.template publish_next<L>();
+      issue_next();
+      issue_next();
+    }
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+    tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    ring.template publish_next<L>();  // E
+    issue_next();                     // the next block's slice 0 into the last slice's slot
+    ring.template publish_next<L>();  // gO
+    ring.template publish_next<L>();  // gO^T
+    const int slot_gt = ring.slot;
+
+    TG tgl;  // layout only
+    TE tel;
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv) {
+      const int vl = wv * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft) {
+        // LDS bases recomputed per block (see opaque_zero): the side tiles sit
+        // in the three slots before and at the current one
+        const int oz = opaque_zero();
+        const char* sGte = smem + oz + slot_gt * SB;
+        const char* sGe = smem + oz + ((slot_gt + NS - 1) % NS) * SB;
+        const char* sEe = smem + oz + ((slot_gt + NS - 2) % NS) * SB;
+        const float* sLe = sLD + oz + (blk & 1) * (2 * BM);
+        const float* sDe = sLe + BM;
+        const int tr0 = wt * WTR + ft * 32;  // first token of the block
+        // dP block = gO[tokens] E[rows]^T over D
+        f32x16_t dp = zero16();
+#pragma unroll
+        for (int kd = 0; kd < DK; ++kd)
+          mfma_k16(dp, read_op(tgl, sGe, tr0 + (lane & 31), kd), read_op(tel, sEe, vl, kd));
+        float dbs = 0.f;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
+          const int tl = tr0 + 8 * g4 + (lane >> 5) * 4;
+          const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
+          const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g4 + i;
+            const float x = sacc[ft][fv][r] * p.scale + bvv[fv];
+            const float pv = fast_exp(x - lv[i]);
+            const float ds = pv * (dp[r] - dv[i]);
+            dbs += ds;
+            sacc[ft][fv][r] = pv;
+            dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
+          }
+        }
+        dbacc[fv] += dbs;
+        if (p.need_stage) {
+          T* dst = stage + (int64_t)(vl0 + vl) * p.ld_stage + n0 + tr0 + (lane >> 5) * 4;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            T q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = from_float<T>(dp[4 * g4 + i]);
+            uint2 u;
+            __builtin_memcpy(&u, q, 8);
+            *reinterpret_cast<uint2*>(dst + g4 * 8) = u;
+          }
+        }
+        if (p.need_dE) {
+          // dE^T[d][v] += gO^T[d][tok] P[tok][v]; registers 8c..8c+7 hold
+          // tokens 16c + 8(t/4) + 4(lane/32) + t%4, stored contiguously in
+          // the gO^T tile (pe_row order): one read per operand
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            V8 bv;
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[ft][fv][8 * c + tt]);
+            const int p0 = tr0 + 8 * (2 * c + (lane >> 5));
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+              const V8 av = *reinterpret_cast<const V8*>(sGte + TGT::elem(db * 32 + (lane & 31), p0));
+              mfma_k16(deacc[db][fv], av, bv);
+            }
+          }
+        }
+        sched_fence();
+      }
+    }
+  }
+  wait_vmcnt<0>();
+
+  // partials of this wave's rows over its token share of the group
+  const int gp = g * C::WT + wt;
+#pragma unroll
+  for (int fv = 0; fv < FV; ++fv) {
+    const int vc = vl0 + wv * WVR + fv * 32 + (lane & 31);  // chunk-local row
+    if (p.need_db) {
+      const float s = wave_sum32(dbacc[fv]);
+      if (lane < 32) p.part_db[(int64_t)gp * p.C + vc] = s;
+    }
+    if (p.need_dE) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = db * 32 + c_row(r, lane);
+          p.part_dE[((int64_t)gp * DP + d) * p.C + vc] = deacc[db][fv][r];
+        }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- GEMMs
 struct GemmParams {
   const void* stage;
@@ -543,13 +785,28 @@ hipError_t fill_zero(void* p, size_t bytes, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The narrow-embedding scores kernel (side tiles carried by the ring) serves
+// bf16 / f16 with DP <= 64; the general one serves the rest.
+template <class T, int DP>
+struct ScoresRing {
+  static constexpr bool value = sizeof(T) == 2 && DP <= 64;
+};
+
 template <class T, int DP>
 hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
-  typedef ScoresTile<T, DP> C;
-  if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
-  timing_begin(kKindBwdScores, stream);
-  bwd_scores_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
-  timing_end(kKindBwdScores, stream);
+  if constexpr (ScoresRing<T, DP>::value) {
+    typedef ScoresRingTile<T, DP> C;
+    if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
+    timing_begin(kKindBwdScores, stream);
+    bwd_scores_ring_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    timing_end(kKindBwdScores, stream);
+  } else {
+    typedef ScoresTile<T, DP> C;
+    if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
+    timing_begin(kKindBwdScores, stream);
+    bwd_scores_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    timing_end(kKindBwdScores, stream);
+  }
   return hipGetLastError();
 }
 
@@ -678,20 +935,31 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   return hipSuccess;
 }
 
+// Tile of the scores kernel that serves (T, DP), and how many workgroups a
+// chunk should have: one per CU for the ring kernel (one fits a CU), two per
+// CU otherwise.
 template <class T, int DP>
-void scores_get(int* BM, int* BV, int* WT) {
-  *BM = ScoresTile<T, DP>::BM;
-  *BV = ScoresTile<T, DP>::BV;
-  *WT = ScoresTile<T, DP>::WT;
+void scores_get(int* BM, int* BV, int* WT, int* wgs) {
+  if constexpr (ScoresRing<T, DP>::value) {
+    *BM = ScoresRingTile<T, DP>::BM;
+    *BV = ScoresRingTile<T, DP>::BV;
+    *WT = ScoresRingTile<T, DP>::WT;
+    *wgs = 256;
+  } else {
+    *BM = ScoresTile<T, DP>::BM;
+    *BV = ScoresTile<T, DP>::BV;
+    *WT = ScoresTile<T, DP>::WT;
+    *wgs = 512;
+  }
 }
 
 template <class T>
-void scores_tile_of(int DP, int* BM, int* BV, int* WT) {
+void scores_tile_of(int DP, int* BM, int* BV, int* WT, int* wgs) {
   switch (DP) {
-    case 32: scores_get<T, 32>(BM, BV, WT); break;
-    case 64: scores_get<T, 64>(BM, BV, WT); break;
-    case 128: scores_get<T, 128>(BM, BV, WT); break;
-    default: scores_get<T, 256>(BM, BV, WT); break;
+    case 32: scores_get<T, 32>(BM, BV, WT, wgs); break;
+    case 64: scores_get<T, 64>(BM, BV, WT, wgs); break;
+    case 128: scores_get<T, 128>(BM, BV, WT, wgs); break;
+    default: scores_get<T, 256>(BM, BV, WT, wgs); break;
   }
 }
 
@@ -704,14 +972,14 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan) {
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
-  int BM, BV, GM, GN, WT;
+  int BM, BV, GM, GN, WT, wgs;
   if (dtype == kF32) {
     if (DP > 128) return false;
-    scores_tile_of<float>(DP, &BM, &BV, &WT);
+    scores_tile_of<float>(DP, &BM, &BV, &WT, &wgs);
     GM = GemmTile<float>::GM;
     GN = GemmTile<float>::GN;
   } else if (dtype == kBF16 || dtype == kF16) {
-    scores_tile_of<bf16_t>(DP, &BM, &BV, &WT);
+    scores_tile_of<bf16_t>(DP, &BM, &BV, &WT, &wgs);
     GM = GemmTile<bf16_t>::GM;
     GN = GemmTile<bf16_t>::GN;
   } else {
@@ -731,7 +999,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->C = c;
   plan->n_chunks = (int)((V + c - 1) / c);
   const int n_vtc = (int)(c / BV);
-  int G = (512 + n_vtc - 1) / n_vtc;
+  int G = wgs == 256 ? wgs / n_vtc : (wgs + n_vtc - 1) / n_vtc;
   if (G > plan->n_tb) G = plan->n_tb;
   if (G < 1) G = 1;
   plan->G = G;

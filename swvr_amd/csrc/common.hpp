@@ -278,10 +278,12 @@ struct KTile {
   __device__ static __forceinline__ int elem(int row, int col) {
     return row * ROWB + (((col / CE) ^ swz(row)) * 16) + (col % CE) * (int)sizeof(T);
   }
-  // Row and first reduction index of this lane's chunk of load i.
-  __device__ static __forceinline__ int row_of(int i) { return ((i * NT + (int)threadIdx.x) * 16) / ROWB; }
-  __device__ static __forceinline__ int kc_of(int i) {
-    const int lin = (i * NT + (int)threadIdx.x) * 16;
+  // Row and first reduction index of the chunk of load i of thread tid.
+  __device__ static __forceinline__ int row_of(int i, int tid = (int)threadIdx.x) {
+    return ((i * NT + tid) * 16) / ROWB;
+  }
+  __device__ static __forceinline__ int kc_of(int i, int tid = (int)threadIdx.x) {
+    const int lin = (i * NT + tid) * 16;
     return (((lin % ROWB) / 16) ^ swz(lin / ROWB)) * CE;
   }
 
@@ -290,18 +292,21 @@ struct KTile {
   int k_valid;
   uint32_t off[NI];  // byte offset of this lane's chunk at k = 0, or kOOB
 
-  __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv) {
+  // tid: this thread's index (a caller that issues a tile rarely may pass a
+  // copy the compiler cannot see through, so that the offsets are computed at
+  // the call instead of being kept live across its loops).
+  __device__ __forceinline__ void setup(const T* b, int64_t ld, int rows_valid, int kv, int tid = (int)threadIdx.x) {
     ldb = ld * (int64_t)sizeof(T);
     k_valid = kv;
-    rebase(b, rows_valid);
+    rebase(b, rows_valid, tid);
   }
   // New rows, same shape.
-  __device__ __forceinline__ void rebase(const T* b, int rows_valid) {
+  __device__ __forceinline__ void rebase(const T* b, int rows_valid, int tid = (int)threadIdx.x) {
     base = reinterpret_cast<const char*>(b);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int row = row_of(i);
-      off[i] = row < rows_valid && row < R ? (uint32_t)(row * ldb + kc_of(i) * (int)sizeof(T)) : kOOB;
+      const int row = row_of(i, tid);
+      off[i] = row < rows_valid && row < R ? (uint32_t)(row * ldb + kc_of(i, tid) * (int)sizeof(T)) : kOOB;
     }
   }
   // Stage the reduction slice [k0, k0 + BK) at LDS address lds.
@@ -565,6 +570,44 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
   if (b >= q * X) return b;
   return (b % X) * q + b / X;
 }
+
+// Workgroup index -> (row, col) of an R x Q tile grid such that the 32
+// workgroups an XCD runs together cover a 4 x 8 patch (4 rows, 8 columns):
+// blocks go to the XCDs round-robin, xcd_swizzle gives each XCD a contiguous
+// range of the tile order, and the order walks 4-row column strips.
+__device__ __forceinline__ void grouped_tile(int b, int R, int Q, int* row, int* col) {
+  constexpr int G = 4;
+  const int t = xcd_swizzle(b, R * Q);
+  const int group = t / (G * Q), first = group * G;
+  const int gsize = min(R - first, G);
+  *row = first + (t % (G * Q)) % gsize;
+  *col = (t % (G * Q)) / gsize;
+}
+
+// An LDS ring of NS slots whose stages are not issued at a uniform rate: the
+// wait that publishes a stage counts the stages actually issued after it
+// (*issued = number of stages issued so far, in stage order; at most 2 of
+// them may stay in flight, L loads per thread each).
+template <int NS>
+struct CountedRing {
+  static constexpr int kDepth = NS;
+  int slot;            // slot of the current stage
+  int cur;             // index of the current stage
+  const int* issued;
+  template <int L>
+  __device__ __forceinline__ void publish_next() {
+    ++cur;
+    const int ahead = *issued - 1 - cur;
+    if (ahead >= 2)
+      wait_vmcnt<2 * L>();
+    else if (ahead == 1)
+      wait_vmcnt<L>();
+    else
+      wait_vmcnt<0>();
+    stage_barrier();
+    slot = slot == NS - 1 ? 0 : slot + 1;
+  }
+};
 
 __device__ __forceinline__ float wave_max32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float wave_sum32(float x) { return x + __shfl_xor(x, 32); }

@@ -59,18 +59,6 @@ __global__ __launch_bounds__(256) void pack_et_kernel(const T* __restrict__ E, i
   if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
 }
 
-// Workgroup index -> (row, col) of an R x Q tile grid such that the 32
-// workgroups an XCD runs together cover a 4 x 8 patch (4 rows, 8 columns):
-// blocks go to the XCDs round-robin, xcd_swizzle gives each XCD a contiguous
-// range of the tile order, and the order walks 4-row column strips.
-__device__ __forceinline__ void grouped_tile(int b, int R, int Q, int* row, int* col) {
-  constexpr int G = 4;
-  const int t = xcd_swizzle(b, R * Q);
-  const int group = t / (G * Q), first = group * G;
-  const int gsize = min(R - first, G);
-  *row = first + (t % (G * Q)) % gsize;
-  *col = (t % (G * Q)) / gsize;
-}
 
 template <class T, int DP>
 __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParams p) {
