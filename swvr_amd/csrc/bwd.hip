@@ -4,11 +4,12 @@
 //   per vocabulary chunk [v0, v0 + C):
 //     P  = exp(s * h W_c^T + b_c - LSE)        (scores recomputed)
 //     dS = P * (gO E_c^T - delta)                                 bwd_scores_kernel
-//       -> stage s*dS in the compute dtype (what the gradient GEMMs consume,
-//          swvr/chunked.py:143-145 / triton_kernels.py:108-109)
+//       -> stage dS in the compute dtype (what the gradient GEMMs consume,
+//          swvr/chunked.py:143-145 / triton_kernels.py:108-109; the
+//          reference stages s*dS, here the GEMMs apply s to their outputs)
 //       -> dE_c = P^T gO and db_c = colsum(dS), accumulated per token group
 //          in registers and written as partials (no atomics)
-//     dW_c = stage^T h   and   dh += stage W_c                    bwd_gemm_kernel
+//     dW_c = s stage^T h   and   dh += s stage W_c                bwd_gemm_kernel
 //     dE_c, db_c = fixed-order sum of the partials                bwd_reduce_kernel
 // Every reduction has a fixed order, so gradients are bitwise reproducible.
 #include "common.hpp"
@@ -79,7 +80,7 @@ struct ScoresParams {
   int v0, cv;           // chunk start and rows
   int C;                // chunk stride of the partials (multiple of BV)
   int n_tb, G, n_vtc;
-  void* stage;          // [C][ld_stage] compute dtype, token index contiguous
+  void* stage;          // [C][ld_stage] dS in the compute dtype, token index contiguous
   int64_t ld_stage;
   float* part_dE;       // [G][DP][C]
   float* part_db;       // [G][C]
@@ -261,12 +262,11 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * g4 + i;
-            const float x = sacc[ft][fv][r] * p.scale + bvv;
-            const float pv = fast_exp(x - lv[i]);
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv) - lv[i]);
             const float ds = pv * (dp[r] - dv[i]);
             dbs += ds;
             sacc[ft][fv][r] = pv;
-            dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
+            dp[r] = ds;  // the gradient GEMMs apply the scale (swvr/chunked.py:143-144)
           }
         }
         dbacc[fv] += dbs;
@@ -516,12 +516,11 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * g4 + i;
-            const float x = sacc[ft][fv][r] * p.scale + bvv[fv];
-            const float pv = fast_exp(x - lv[i]);
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv[fv]) - lv[i]);
             const float ds = pv * (dp[r] - dv[i]);
             dbs += ds;
             sacc[ft][fv][r] = pv;
-            dp[r] = ds * p.scale;  // dL/d(h W^T) (swvr/chunked.py:143-144)
+            dp[r] = ds;  // the gradient GEMMs apply the scale (swvr/chunked.py:143-144)
           }
         }
         dbacc[fv] += dbs;
@@ -600,16 +599,18 @@ struct GemmParams {
   void* gh;
   int gh_dtype;
   int dh_first, dh_last;
+  float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
 };
 
-// Write a GEMM accumulator tile: out[(row_off + row) * ld + col] = acc (+ prev[...]),
+// Write a GEMM accumulator tile: out[(row_off + row) * ld + col] = scale * acc (+ prev[...]),
 // rows < rows, cols < ld.  prev (fp32, may alias out) is added when non-null.
 // prev may alias out (the running fp32 dh): the previous values of a row of
 // blocks are all loaded before any of them is overwritten, so the loads do not
 // wait for one store after another.
 template <int FM, int FN, class OutT>
-__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], OutT* out, const float* prev,
-                                           int64_t row_off, int rows, int row0, int col0, int ld) {
+__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float scale, OutT* out,
+                                           const float* prev, int64_t row_off, int rows, int row0, int col0,
+                                           int ld) {
   const int lane = lane_id();
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
@@ -629,7 +630,7 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], OutT* 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = row0 + fm * 32 + c_row(r, lane);
-        if (row < rows && col < ld) out[(row_off + row) * ld + col] = (OutT)(acc[fm][fn][r] + pv[fn][r]);
+        if (row < rows && col < ld) out[(row_off + row) * ld + col] = (OutT)fmaf(acc[fm][fn][r], scale, pv[fn][r]);
       }
     }
   }
@@ -709,21 +710,21 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   // dispatch on the output dtype outside the unrolled store loops
   if constexpr (DW) {
     if (p.gW_dtype == kBF16)
-      gemm_store<FM, FN>(acc, static_cast<bf16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<bf16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
     else if (p.gW_dtype == kF16)
-      gemm_store<FM, FN>(acc, static_cast<f16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<f16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
     else
-      gemm_store<FM, FN>(acc, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
   } else {
     const float* prev = p.dh_first ? nullptr : p.dh_acc;
     if (!p.dh_last)
-      gemm_store<FM, FN>(acc, p.dh_acc, prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K);
     else if (p.gh_dtype == kBF16)
-      gemm_store<FM, FN>(acc, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
     else if (p.gh_dtype == kF16)
-      gemm_store<FM, FN>(acc, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
     else
-      gemm_store<FM, FN>(acc, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
   }
 }
 
@@ -920,6 +921,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.gh_dtype = p.gh_dtype;
       gp.dh_first = c == 0;
       gp.dh_last = c == plan.n_chunks - 1;
+      gp.scale = p.scale;
       if ((e = dispatch_gemm<T>(plan, gp, stream)) != hipSuccess) return e;
     }
     if (p.gE || p.gb) {

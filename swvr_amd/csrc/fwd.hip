@@ -169,7 +169,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int ft = 0; ft < FT; ++ft) {
-            const float x = sacc[fv][ft][4 * g + i] * p.scale + bb[i];
+            const float x = fmaf(sacc[fv][ft][4 * g + i], p.scale, bb[i]);  // rounded as the backward rounds it
             sacc[fv][ft][4 * g + i] = x;
             mx[ft] = fmaxf(mx[ft], x);
           }
