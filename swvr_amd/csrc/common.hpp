@@ -309,19 +309,20 @@ struct KTile {
       off[i] = row < rows_valid && row < R ? (uint32_t)(row * ldb + kc_of(i, tid) * (int)sizeof(T)) : kOOB;
     }
   }
-  // Stage the reduction slice [k0, k0 + BK) at LDS address lds.
+  // Stage the reduction slice [k0, k0 + BK) at LDS address lds.  The whole-
+  // slice path and the tail path are separate load batches, so the steady
+  // state computes no per-lane bounds.
   __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
     const rsrc_t r = make_rsrc(base + (int64_t)k0 * (int)sizeof(T));
-    uint32_t v[NI];
+    if (PARTIAL && (int)threadIdx.x * 16 >= BYTES) return;  // wave-uniform
     if (k0 + BK <= k_valid) {
-#pragma unroll
-      for (int i = 0; i < NI; ++i) v[i] = off[i];
+      dma_n<NI, NT * 16>(r, off, lds + wave_id() * 1024);
     } else {
+      uint32_t v[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) v[i] = k0 + kc_of(i) >= k_valid ? kOOB : off[i];
+      dma_n<NI, NT * 16>(r, v, lds + wave_id() * 1024);
     }
-    if (PARTIAL && (int)threadIdx.x * 16 >= BYTES) return;  // wave-uniform
-    dma_n<NI, NT * 16>(r, v, lds + wave_id() * 1024);
   }
 };
 
@@ -360,15 +361,14 @@ struct RTile {
   }
   __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
     const rsrc_t rs = make_rsrc(base + (int64_t)k0 * ldb);
-    uint32_t v[NI];
     if (k0 + BK <= k_valid) {
-#pragma unroll
-      for (int i = 0; i < NI; ++i) v[i] = off[i];
+      dma_n<NI, NT * 16>(rs, off, lds + wave_id() * 1024);
     } else {
+      uint32_t v[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) v[i] = k0 + kr_of(i) >= k_valid ? kOOB : off[i];
+      dma_n<NI, NT * 16>(rs, v, lds + wave_id() * 1024);
     }
-    dma_n<NI, NT * 16>(rs, v, lds + wave_id() * 1024);
   }
 };
 
@@ -447,22 +447,95 @@ __global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E
   if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
 }
 
+// Per-lane byte offsets, within one staged slice, of the operands of F
+// fragments (rows row0 + 32 f + lane % 32) for the J k16 steps of a slice,
+// computed once per reduction so that an operand read is one add of the
+// slice base plus the LDS read(s).
+//   KTile: one offset per (step, fragment) (the XOR swizzle mixes the step
+//          into the chunk index);
+//   RTile (2-byte types): one offset per fragment; the step adds 16 k-rows
+//          and the second half of the operand 4 k-rows, both immediate
+//          offsets of the transposing reads (the swizzle depends only on the
+//          k-row modulo 4, which neither changes).
+template <class Tile, int F, int J>
+struct OpOffsets;
+
+template <class T, int R, int BK, int NT, int F, int J>
+struct OpOffsets<KTile<T, R, BK, NT>, F, J> {
+  typedef KTile<T, R, BK, NT> KT;
+  typedef typename Vec8<T>::type V8;
+  uint32_t off[J][F];
+  __device__ __forceinline__ void init(int row0) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int f = 0; f < F; ++f) off[j][f] = KT::elem(row0 + 32 * f + (lane & 31), 16 * j + (lane >> 5) * 8);
+  }
+  __device__ __forceinline__ V8 read(const char* stage, int j, int f) const {
+    if constexpr (sizeof(T) == 2) {
+      return *reinterpret_cast<const V8*>(stage + off[j][f]);
+    } else {
+      // 8 fp32 values span chunks c and c + 1 = c ^ 1 (c even): offsets o and o ^ 16
+      const float4 lo = *reinterpret_cast<const float4*>(stage + off[j][f]);
+      const float4 hi = *reinterpret_cast<const float4*>(stage + (off[j][f] ^ 16u));
+      V8 v;
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+      return v;
+    }
+  }
+};
+
+template <class T, int R, int BK, int NT, int F, int J>
+struct OpOffsets<RTile<T, R, BK, NT>, F, J> {
+  typedef RTile<T, R, BK, NT> RT;
+  typedef typename Vec8<T>::type V8;
+  int row0;
+  uint32_t off[F];
+  __device__ __forceinline__ void init(int r0) {
+    row0 = r0;
+    if constexpr (sizeof(T) == 2) {
+      // lane = 32 hi + 16 g + 4 a + q reads k-row 8 hi + a (+ 16 j + 4 h) at
+      // row chunk (row0 + 32 f) / 8 + 2 g + q / 2, XOR 4 a, half q % 2
+      const int lane = lane_id();
+      const int hi = lane >> 5, g = (lane >> 4) & 1, a = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+      for (int f = 0; f < F; ++f)
+        off[f] = (uint32_t)((8 * hi + a) * RT::ROWB + ((((row0 + 32 * f) >> 3) + 2 * g + (q >> 1)) ^ (4 * a)) * 16 +
+                            8 * (q & 1));
+    }
+  }
+  __device__ __forceinline__ V8 read(const char* stage, int j, int f) const {
+    if constexpr (sizeof(T) == 2) {
+      const char* p = stage + off[f] + j * 16 * RT::ROWB;
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+      const s16x4_t hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p + 4 * RT::ROWB));
+      const s16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      V8 out;
+      __builtin_memcpy(&out, &both, 16);
+      return out;
+    } else {
+      return read_op(RT(), stage, row0 + 32 * f + (lane_id() & 31), j);
+    }
+  }
+};
+
 // MFMA operands of one k16 step of a wave's FM x FN grid of 32x32 blocks.
 template <class T, int FM, int FN>
 struct StepOps {
   typename Vec8<T>::type a[FM], b[FN];
 };
 
-// Read the operands of k16 step j of a staged slice (A rows a_row0 + 32 fm +
-// lane % 32, B rows b_row0 + 32 fn + lane % 32).
-template <class T, int FM, int FN, class TA, class TB>
-__device__ __forceinline__ void load_step(StepOps<T, FM, FN>& o, const TA& ta, const TB& tb, const char* sA,
-                                          const char* sB, int a_row0, int b_row0, int j) {
-  const int lr = lane_id() & 31;
+// Read the operands of k16 step j of a staged slice.
+template <class T, int FM, int FN, class OA, class OB>
+__device__ __forceinline__ void load_step(StepOps<T, FM, FN>& o, const OA& ao, const OB& bo, const char* sA,
+                                          const char* sB, int j) {
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) o.a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
+  for (int fm = 0; fm < FM; ++fm) o.a[fm] = ao.read(sA, j, fm);
 #pragma unroll
-  for (int fn = 0; fn < FN; ++fn) o.b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+  for (int fn = 0; fn < FN; ++fn) o.b[fn] = bo.read(sB, j, fn);
 }
 
 template <class T, int FM, int FN>
@@ -479,18 +552,17 @@ __device__ __forceinline__ void mma_step(f32x16_t (&acc)[FM][FN], const StepOps<
 // that uses its predecessor, so only one A operand is double-buffered at a
 // time (register budget) while every read still has at least the rest of the
 // step's MFMAs to land.
-template <class T, int FM, int FN, class TA, class TB>
+template <class T, int FM, int FN, class OA, class OB>
 __device__ __forceinline__ void mma_load_step(f32x16_t (&acc)[FM][FN], const StepOps<T, FM, FN>& cur,
-                                              StepOps<T, FM, FN>& nxt, const TA& ta, const TB& tb, const char* sA,
-                                              const char* sB, int a_row0, int b_row0, int j) {
-  const int lr = lane_id() & 31;
+                                              StepOps<T, FM, FN>& nxt, const OA& ao, const OB& bo, const char* sA,
+                                              const char* sB, int j) {
 #pragma unroll
-  for (int fn = 0; fn < FN; ++fn) nxt.b[fn] = read_op(tb, sB, b_row0 + fn * 32 + lr, j);
+  for (int fn = 0; fn < FN; ++fn) nxt.b[fn] = bo.read(sB, j, fn);
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) mfma_k16(acc[fm][fn], cur.a[fm], cur.b[fn]);
-    nxt.a[fm] = read_op(ta, sA, a_row0 + fm * 32 + lr, j);
+    nxt.a[fm] = ao.read(sA, j, fm);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -527,10 +599,14 @@ template <class T, int BK, int L, int FM, int FN, class TA, class TB, class R, c
 __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* smem,
                                             int sb, R& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
   constexpr int J = BK / 16;
+  OpOffsets<TA, FM, J> ao;
+  ao.init(a_row0);
+  OpOffsets<TB, FN, J> bo;
+  bo.init(b_row0);
   StepOps<T, FM, FN> cur, nxt;
   {
     const char* sA = smem + ring.slot * sb;
-    load_step(cur, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, 0);
+    load_step(cur, ao, bo, sA, sA + TA::BYTES, 0);
   }
   // all stages but the last: the next stage is published between the last
   // two k16 steps (the last stage is peeled so no branch splits the MFMAs)
@@ -539,14 +615,14 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
     issue_next();
 #pragma unroll
     for (int j = 0; j + 1 < J; ++j) {
-      mma_load_step(acc, cur, nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
+      mma_load_step(acc, cur, nxt, ao, bo, sA, sA + TA::BYTES, j + 1);
       cur = nxt;
     }
     __builtin_amdgcn_sched_barrier(0);  // the MFMAs above stay ahead of the barrier,
     ring.template publish_next<L>();
     __builtin_amdgcn_sched_barrier(0);  // the ones below stay behind it
     const char* nA = smem + ring.slot * sb;
-    mma_load_step(acc, cur, nxt, ta, tb, nA, nA + TA::BYTES, a_row0, b_row0, 0);
+    mma_load_step(acc, cur, nxt, ao, bo, nA, nA + TA::BYTES, 0);
     cur = nxt;
   }
   {
@@ -554,7 +630,7 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
     issue_next();
 #pragma unroll
     for (int j = 0; j + 1 < J; ++j) {
-      mma_load_step(acc, cur, nxt, ta, tb, sA, sA + TA::BYTES, a_row0, b_row0, j + 1);
+      mma_load_step(acc, cur, nxt, ao, bo, sA, sA + TA::BYTES, j + 1);
       cur = nxt;
     }
     mma_step(acc, cur);
