@@ -4,7 +4,7 @@
 //   per vocabulary chunk [v0, v0 + C):
 //     P  = exp(s * h W_c^T + b_c - LSE)        (scores recomputed)
 //     dS = P * (gO E_c^T - delta)                                 bwd_scores_kernel
-//       -> stage dS in the compute dtype (what the gradient GEMMs consume,
+//       -> stage dS in the compute dtype, in 32 x 32 blocks (what the gradient GEMMs consume,
 //          swvr/chunked.py:143-145 / triton_kernels.py:108-109; the
 //          reference stages s*dS, here the GEMMs apply s to their outputs)
 //       -> dE_c = P^T gO and db_c = colsum(dS), accumulated per token group
@@ -80,12 +80,47 @@ struct ScoresParams {
   int v0, cv;           // chunk start and rows
   int C;                // chunk stride of the partials (multiple of BV)
   int n_tb, G, n_vtc;
-  void* stage;          // [C][ld_stage] dS in the compute dtype, token index contiguous
-  int64_t ld_stage;
+  void* stage;          // dS in the compute dtype, tiled (stage_off)
+  int n_tb32;           // N_pad / 32: 32-token blocks of the stage
   float* part_dE;       // [G][DP][C]
   float* part_db;       // [G][C]
   int need_stage, need_dE, need_db;
 };
+
+// ---------------------------------------------------------------- dS stage layout
+// The stage holds dS in 32 x 32 blocks, [C / 32][N_pad / 32][32 vocabulary
+// rows][32 positions], each block contiguous (2 KB in bf16).  Position p of a
+// block holds token stage_tok(p) of its 32 tokens: the order in which a lane
+// of an MFMA accumulator holds tokens (register 4g + i of lane half hi is
+// token 8g + 4hi + i), so a lane stores its 16 values as one run and a wave
+// one whole block.  The gradient GEMMs reduce over positions (dW, with the
+// matching rows of h) or produce rows in position order (dh, written back to
+// their tokens).
+__host__ __device__ __forceinline__ int stage_tok(int p) { return 8 * ((p & 15) >> 2) + 4 * (p >> 4) + (p & 3); }
+// Element offset of (chunk-local vocabulary row v, position q).
+__host__ __device__ __forceinline__ int64_t stage_off(int v, int q, int n_tb32) {
+  return ((int64_t)(v >> 5) * n_tb32 + (q >> 5)) * 1024 + (v & 31) * 32 + (q & 31);
+}
+
+// One 32 x 32 accumulator block of dS (lane column: vocabulary row vc,
+// registers: the block's 32 tokens from tok0) into the stage.
+template <class T>
+__device__ __forceinline__ void store_ds_block(const f32x16_t& ds, void* stage, int n_tb32, int vc, int tok0) {
+  T* dst = static_cast<T*>(stage) + stage_off(vc, tok0, n_tb32) + (lane_id() >> 5) * 16;
+  if constexpr (sizeof(T) == 2) {
+    T q[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) q[r] = from_float<T>(ds[r]);
+    uint4 u[2];
+    __builtin_memcpy(u, q, 32);
+    reinterpret_cast<uint4*>(dst)[0] = u[0];
+    reinterpret_cast<uint4*>(dst)[1] = u[1];
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      reinterpret_cast<float4*>(dst)[g] = make_float4(ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]);
+  }
+}
 
 // Tile shape of the scores kernel per (dtype, padded D): BM tokens x BV
 // vocabulary rows per workgroup of WT x WV waves (two waves per SIMD for
@@ -197,7 +232,6 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue_next();
 
-  T* stage = static_cast<T*>(p.stage);
   f32x16_t sacc[FT][FV];
   Ring<NS> ring{NS - 1, n_blocks * nk};  // the first publish_next() moves to stage 0, slot 0
   for (int blk = 0; blk < n_blocks; ++blk) {
@@ -270,23 +304,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
           }
         }
         dbacc[fv] += dbs;
-        if (p.need_stage) {
-          T* dst = stage + (int64_t)(vl0 + vl) * p.ld_stage + n0 + tr0 + (lane >> 5) * 4;
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            if constexpr (sizeof(T) == 2) {
-              T q[4];
-#pragma unroll
-              for (int i = 0; i < 4; ++i) q[i] = from_float<T>(dp[4 * g4 + i]);
-              uint2 u;
-              __builtin_memcpy(&u, q, 8);
-              *reinterpret_cast<uint2*>(dst + g4 * 8) = u;
-            } else {
-              *reinterpret_cast<float4*>(dst + g4 * 8) =
-                  make_float4(dp[4 * g4], dp[4 * g4 + 1], dp[4 * g4 + 2], dp[4 * g4 + 3]);
-            }
-          }
-        }
+        if (p.need_stage) store_ds_block<T>(dp, p.stage, p.n_tb32, vl0 + vl, n0 + tr0);
         if (p.need_dE) {
           // dE^T[d][v] += gO^T[d][tok] P[tok][v]; registers 8c..8c+7 hold
           // tokens 16c + 8(t/4) + 4(lane/32) + t%4, stored contiguously in
@@ -460,7 +478,6 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue_next();
 
-  T* stage = static_cast<T*>(p.stage);
   f32x16_t sacc[FT][FV];
   CountedRing<NS> ring{NS - 1, -1, &issued};
   ring.template publish_next<L>();  // block 0, slice 0
@@ -524,18 +541,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
           }
         }
         dbacc[fv] += dbs;
-        if (p.need_stage) {
-          T* dst = stage + (int64_t)(vl0 + vl) * p.ld_stage + n0 + tr0 + (lane >> 5) * 4;
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            T q[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) q[i] = from_float<T>(dp[4 * g4 + i]);
-            uint2 u;
-            __builtin_memcpy(&u, q, 8);
-            *reinterpret_cast<uint2*>(dst + g4 * 8) = u;
-          }
-        }
+        if (p.need_stage) store_ds_block<T>(dp, p.stage, p.n_tb32, vl0 + vl, n0 + tr0);
         if (p.need_dE) {
           // dE^T[d][v] += gO^T[d][tok] P[tok][v]; registers 8c..8c+7 hold
           // tokens 16c + 8(t/4) + 4(lane/32) + t%4, stored contiguously in
@@ -582,8 +588,8 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 
 // ---------------------------------------------------------------- GEMMs
 struct GemmParams {
-  const void* stage;
-  int64_t ld_stage;
+  const void* stage;  // tiled dS (stage_off)
+  int n_tb32;
   int64_t N_pad;
   const void* h;
   int64_t ldh;
@@ -607,7 +613,9 @@ struct GemmParams {
 // prev may alias out (the running fp32 dh): the previous values of a row of
 // blocks are all loaded before any of them is overwritten, so the loads do not
 // wait for one store after another.
-template <int FM, int FN, class OutT>
+// POS: the tile's rows are stage positions (row0 multiple of 32), written to
+// their tokens.
+template <int FM, int FN, bool POS = false, class OutT>
 __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float scale, OutT* out,
                                            const float* prev, int64_t row_off, int rows, int row0, int col0,
                                            int ld) {
@@ -620,7 +628,7 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float 
       const int col = col0 + fn * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = row0 + fm * 32 + c_row(r, lane);
+        const int row = row0 + fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
         pv[fn][r] = (prev && row < rows && col < ld) ? prev[(row_off + row) * ld + col] : 0.f;
       }
     }
@@ -629,12 +637,105 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float 
       const int col = col0 + fn * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = row0 + fm * 32 + c_row(r, lane);
+        const int row = row0 + fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
         if (row < rows && col < ld) out[(row_off + row) * ld + col] = (OutT)fmaf(acc[fm][fn][r], scale, pv[fn][r]);
       }
     }
   }
 }
+
+// Tile loaders of the gradient GEMMs over the tiled stage (the LDS layouts of
+// KTile / RTile, so the operand reads are the same).
+// dW, A: rows = vocabulary rows from v0 (multiple of 32, rows_valid of them
+// in the chunk), k = positions.
+template <class T, int R, int BK, int NT>
+struct StageKLoader {
+  typedef KTile<T, R, BK, NT> Layout;
+  static constexpr int BYTES = Layout::BYTES, NI = Layout::NI, NI_MIN = Layout::NI_MIN;
+  static_assert(!Layout::PARTIAL && 32 % BK == 0, "whole loads, slices inside a block");
+  const char* base;
+  uint32_t off[NI];
+  __device__ __forceinline__ void setup(const void* stage, int v0, int rows_valid, int n_tb32) {
+    base = static_cast<const char*>(stage) + stage_off(v0, 0, n_tb32) * (int)sizeof(T);
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      off[i] = Layout::row_of(i) < rows_valid
+                   ? (uint32_t)(stage_off(Layout::row_of(i), Layout::kc_of(i), n_tb32) * (int)sizeof(T))
+                   : kOOB;
+  }
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
+    const rsrc_t r = make_rsrc(base + ((int64_t)(k0 >> 5) * 1024 + (k0 & 31)) * (int)sizeof(T));
+    dma_n<NI, NT * 16>(r, off, lds + wave_id() * 1024);
+  }
+};
+
+// dh, A: rows = positions from q0 (multiple of 32), k = vocabulary rows.
+// Every vocabulary row a slice reaches (below the chunk's rows rounded up to
+// the scores tile) holds dS, zero past the chunk, so no bounds apply.
+template <class T, int R, int BK, int NT>
+struct StageRLoader {
+  typedef RTile<T, R, BK, NT> Layout;
+  static constexpr int BYTES = Layout::BYTES, NI = Layout::NI, NI_MIN = Layout::NI_MIN;
+  static_assert(32 % BK == 0, "slices inside a block");
+  const char* base;
+  int n_tb32;
+  uint32_t off[NI];
+  __device__ __forceinline__ void setup(const void* stage, int q0, int ntb) {
+    n_tb32 = ntb;
+    base = static_cast<const char*>(stage) + stage_off(0, q0, ntb) * (int)sizeof(T);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int lin = (i * NT + (int)threadIdx.x) * 16;
+      const int kr = lin / Layout::ROWB;
+      const int r = (((lin % Layout::ROWB) / 16) ^ Layout::swz(kr)) * Layout::CE;
+      off[i] = (uint32_t)(stage_off(kr, r, ntb) * (int)sizeof(T));
+    }
+  }
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
+    const rsrc_t r = make_rsrc(base + stage_off(k0, 0, n_tb32) * (int)sizeof(T));
+    dma_n<NI, NT * 16>(r, off, lds + wave_id() * 1024);
+  }
+};
+
+// dW, B: h with the k-rows (tokens) of each 32-token block in position order.
+template <class T, int R, int BK, int NT>
+struct PosRLoader {
+  typedef RTile<T, R, BK, NT> Layout;
+  static constexpr int BYTES = Layout::BYTES, NI = Layout::NI, NI_MIN = Layout::NI_MIN;
+  const char* base;
+  int64_t ldb;
+  int k_valid;
+  uint32_t col[NI];  // column byte offset of this lane's chunk, or kOOB
+  uint32_t off[NI];  // offset at a block start (k0 % 32 == 0), kOOB for absent columns
+  __device__ __forceinline__ void setup(const T* b, int64_t ld, int cols_valid, int kv) {
+    base = reinterpret_cast<const char*>(b);
+    ldb = ld * (int64_t)sizeof(T);
+    k_valid = kv;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int lin = (i * NT + (int)threadIdx.x) * 16;
+      const int kr = lin / Layout::ROWB;
+      const int r = (((lin % Layout::ROWB) / 16) ^ Layout::swz(kr)) * Layout::CE;
+      col[i] = r < cols_valid ? (uint32_t)(r * (int)sizeof(T)) : kOOB;
+      off[i] = r < cols_valid ? (uint32_t)(stage_tok(kr & 31) * ldb + r * (int)sizeof(T)) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
+    const int kb = k0 & ~31;
+    const rsrc_t rs = make_rsrc(base + (int64_t)kb * ldb);
+    if (BK == 32 && kb + 32 <= k_valid) {
+      dma_n<NI, NT * 16>(rs, off, lds + wave_id() * 1024);
+    } else {
+      uint32_t v[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int t = stage_tok((k0 & 31) + Layout::kr_of(i));
+        v[i] = (col[i] == kOOB || kb + t >= k_valid) ? kOOB : (uint32_t)(t * ldb) + col[i];
+      }
+      dma_n<NI, NT * 16>(rs, v, lds + wave_id() * 1024);
+    }
+  }
+};
 
 // Single-tile pipelined reduction: acc += A[.., 0:k_total] B[.., 0:k_total]^T.
 template <class T, int BK, int FM, int FN, class TA, class TB>
@@ -674,9 +775,10 @@ struct GemmTile {
   static constexpr int NT = 64 * WM * WN;
 };
 
-// One tile of one gradient product; DW selects the product:
-//   DW:  dW[v0+v][k]  = sum_tok stage[v][tok] h[tok][k]     (A: KTile, B: RTile)
-//   !DW: dh[tok][k]  += sum_v  stage[v][tok] W[v0+v][k]      (A: RTile, B: RTile)
+// One tile of one gradient product; DW selects the product (q: stage
+// positions, tok(q) their tokens):
+//   DW:  dW[v0+v][k]    = s sum_q stage[v][q] h[tok(q)][k]    (A: KTile layout, B: RTile layout)
+//   !DW: dh[tok(q)][k] += s sum_v stage[v][q] W[v0+v][k]      (A: RTile layout, B: RTile layout)
 template <class T, bool DW>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem) {
   typedef GemmTile<T> G;
@@ -686,21 +788,22 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   const int w = wave_id();
   const int wm = w / G::WN, wn = w % G::WN;
   const int mt = t / p.n_n, nt = t % p.n_n;
-  const T* stage = static_cast<const T*>(p.stage);
   f32x16_t acc[FM][FN];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = zero16();
-  RTile<T, GN, kBK, NT> tb;
   if constexpr (DW) {
-    KTile<T, GM, kBK, NT> ta;
-    ta.setup(stage + (int64_t)mt * GM * p.ld_stage, p.ld_stage, p.cv - mt * GM, p.N);
+    StageKLoader<T, GM, kBK, NT> ta;
+    ta.setup(p.stage, mt * GM, p.cv - mt * GM, p.n_tb32);
+    PosRLoader<T, GN, kBK, NT> tb;
     tb.setup(static_cast<const T*>(p.h) + nt * GN, p.ldh, p.K - nt * GN, p.N);
-    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.N, wm * (GM / G::WM), wn * (GN / G::WN));
+    // whole 32-position blocks: a partial block's tokens sit anywhere in it
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (p.N + 31) & ~31, wm * (GM / G::WM), wn * (GN / G::WN));
   } else {
-    RTile<T, GM, kBK, NT> ta;
-    ta.setup(stage + (int64_t)mt * GM, p.ld_stage, (int)(p.N_pad - (int64_t)mt * GM), p.cv);
+    StageRLoader<T, GM, kBK, NT> ta;
+    ta.setup(p.stage, mt * GM, p.n_tb32);
+    RTile<T, GN, kBK, NT> tb;
     tb.setup(static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);
     gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / G::WM), wn * (GN / G::WN));
   }
@@ -718,13 +821,13 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   } else {
     const float* prev = p.dh_first ? nullptr : p.dh_acc;
     if (!p.dh_last)
-      gemm_store<FM, FN>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN, true>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K);
     else if (p.gh_dtype == kBF16)
-      gemm_store<FM, FN>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN, true>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
     else if (p.gh_dtype == kF16)
-      gemm_store<FM, FN>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN, true>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
     else
-      gemm_store<FM, FN>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<FM, FN, true>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
   }
 }
 
@@ -890,7 +993,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.G = plan.G;
     sp.n_vtc = (cv + plan.BV - 1) / plan.BV;
     sp.stage = stage;
-    sp.ld_stage = plan.N_pad;
+    sp.n_tb32 = (int)(plan.N_pad / 32);
     sp.part_dE = part_dE;
     sp.part_db = part_db;
     sp.need_stage = need_stage;
@@ -901,7 +1004,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if (need_stage) {
       GemmParams gp;
       gp.stage = stage;
-      gp.ld_stage = plan.N_pad;
+      gp.n_tb32 = (int)(plan.N_pad / 32);
       gp.N_pad = plan.N_pad;
       gp.h = p.h;
       gp.ldh = p.ldh;

@@ -260,6 +260,7 @@ __device__ __forceinline__ void wait_stages(int ahead) {
 
 template <class T, int R, int BK, int NT = kThreads>
 struct KTile {
+  typedef KTile Layout;                             // LDS layout (operand reads)
   static constexpr int CE = 16 / (int)sizeof(T);    // elements per chunk
   static constexpr int CPR = BK / CE;               // chunks per LDS row
   static constexpr int ROWB = BK * (int)sizeof(T);  // bytes per LDS row
@@ -328,6 +329,7 @@ struct KTile {
 
 template <class T, int R, int BK, int NT = kThreads>
 struct RTile {
+  typedef RTile Layout;                             // LDS layout (operand reads)
   static constexpr int CE = 16 / (int)sizeof(T);
   static constexpr int ROWB = R * (int)sizeof(T);  // bytes per LDS k-row
   static constexpr int BYTES = BK * ROWB;
@@ -599,9 +601,9 @@ template <class T, int BK, int L, int FM, int FN, class TA, class TB, class R, c
 __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb, const char* smem,
                                             int sb, R& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
   constexpr int J = BK / 16;
-  OpOffsets<TA, FM, J> ao;
+  OpOffsets<typename TA::Layout, FM, J> ao;
   ao.init(a_row0);
-  OpOffsets<TB, FN, J> bo;
+  OpOffsets<typename TB::Layout, FN, J> bo;
   bo.init(b_row0);
   StepOps<T, FM, FN> cur, nxt;
   {
