@@ -65,8 +65,8 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__
 
 // ---------------------------------------------------------------- scores
 struct ScoresParams {
-  const void* h;
-  int64_t ldh;
+  const void* hp;       // h packed in its tiles' LDS image (pack_rows_kernel)
+  int hS;               // its reduction slices
   const void* W;
   int64_t ldw;
   const void* Ep;       // packed E [V_pad][DP]
@@ -154,7 +154,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   constexpr int kBK = SliceK<T>::value;
   constexpr int BM = C::BM, BV = C::BV, NT = C::NT;
   constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
-  typedef KTile<T, BM, kBK, NT> TA;  // h rows of the token block
+  typedef PackedKLoader<T, BM, kBK, NT> TA;  // h rows of the token block (packed)
   typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
   typedef KTile<T, BV, DP, NT> TE;   // E tile
   typedef KTile<T, BM, DP, NT> TG;   // gO tile
@@ -207,9 +207,8 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
   const int n_blocks = tb_end - tb_begin;
-  const T* h = static_cast<const T*>(p.h);
   TA ta;
-  ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
+  ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
   tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
   // issue cursor: the next stage to load (NS - 1 ahead of the compute)
@@ -218,7 +217,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
     if (is_blk >= n_blocks) return;
     if (is_kt == 0) {
       const int n0 = (tb_begin + is_blk) * BM;
-      ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
+      ta.rebase(n0);
     }
     const uint32_t st = lds0 + is_slot * SB;
     ta.issue(st, is_kt * kBK);
@@ -378,7 +377,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   constexpr int kBK = SliceK<T>::value;
   constexpr int BM = C::BM, BV = C::BV, NT = C::NT, NS = C::NS;
   constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
-  typedef KTile<T, BM, kBK, NT> TA;  // h rows of the token block
+  typedef PackedKLoader<T, BM, kBK, NT> TA;  // h rows of the token block (packed)
   typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
   typedef KTile<T, BV, DP, NT> TE;   // E tile
   typedef KTile<T, BM, DP, NT> TG;   // gO tile
@@ -418,11 +417,10 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
   const int per_blk = nk + 3;
   const int total = n_blocks * per_blk;
-  const T* h = static_cast<const T*>(p.h);
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsL = lds0 + NS * SB;
   TA ta;
-  ta.setup(h + (int64_t)tb_begin * BM * p.ldh, p.ldh, p.N - tb_begin * BM, p.K);
+  ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
   tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
   const rsrc_t r_none = make_rsrc(nullptr);
@@ -440,7 +438,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
     const int n0 = (tb_begin + is_blk) * BM;
     if (is_sub < nk) {
       if (is_sub == 0) {
-        ta.rebase(h + (int64_t)n0 * p.ldh, p.N - n0);
+        ta.rebase(n0);
         // LSE and delta of the block into strip (block & 1), ahead of its slices
         const int c = threadIdx.x;
         if (c < BM / 2) {
@@ -951,6 +949,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   float* lsed = reinterpret_cast<float*>(ws + plan.off_lsed);
   T* Ep = reinterpret_cast<T*>(ws + plan.off_Ep);
   float* biasp = reinterpret_cast<float*>(ws + plan.off_bias);
+  T* hp = reinterpret_cast<T*>(ws + plan.off_hp);
 
   {
     const int64_t n = (int64_t)plan.N_pad * plan.DP;
@@ -964,6 +963,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     timing_begin(kKindPack, stream);
     pack_vocab_kernel<T><<<(int)((nv + 255) / 256), 256, 0, stream>>>(
         static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp);
+    const int64_t chunks = (int64_t)plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
+    pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
+        static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, hp);
     timing_end(kKindPack, stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -973,8 +975,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     const int v0 = (int)(c * plan.C);
     const int cv = (int)((p.V - v0) < plan.C ? (p.V - v0) : plan.C);
     ScoresParams sp;
-    sp.h = p.h;
-    sp.ldh = p.ldh;
+    sp.hp = hp;
+    sp.hS = plan.hS;
     sp.W = p.W;
     sp.ldw = p.ldw;
     sp.Ep = Ep;
@@ -1131,6 +1133,10 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->V_pad * DP * tb);
   plan->off_bias = off;
   off += align256((size_t)plan->V_pad * 4);
+  const int bk = dtype == kF32 ? SliceK<float>::value : SliceK<bf16_t>::value;
+  plan->hS = packed_slices(K, bk);
+  plan->off_hp = off;
+  off += align256((size_t)plan->N_pad * plan->hS * bk * tb);
   plan->ws_bytes = off;
   return true;
 }

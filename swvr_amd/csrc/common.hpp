@@ -687,6 +687,76 @@ struct CountedRing {
   }
 };
 
+// ----------------------------------------------------------------------------
+// Token rows (h) packed in the LDS image of their operand tiles:
+// [N_pad / 32][S = K_pad / BK][32 rows][BK], each 16-byte chunk already at its
+// XOR-swizzled place (KTile layout), zeros past N and K.  A tile of any
+// multiple of 32 rows then loads a reduction slice as contiguous 2 KB runs
+// (full cache lines instead of one 64-byte piece per row) with no bounds.
+template <class T>
+__global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ src, int64_t ld, int N, int K, int S,
+                                                        int64_t n_chunks, T* __restrict__ dst) {
+  constexpr int BK = SliceK<T>::value, CE = 16 / (int)sizeof(T), CPR = BK / CE;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_chunks;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t per_group = (int64_t)S * 32 * CPR;
+    const int64_t grp = e / per_group;
+    const int rem = (int)(e - grp * per_group);
+    const int s = rem / (32 * CPR), lin = rem % (32 * CPR);
+    const int row = lin / CPR, pc = lin % CPR;
+    const int64_t n = grp * 32 + row;
+    const int k = s * BK + (pc ^ chunk_swizzle(row, CPR)) * CE;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (n < N) {
+      if (k + CE <= K) {
+        v = *reinterpret_cast<const uint4*>(src + n * ld + k);
+      } else if (k < K) {
+        T t[CE];
+#pragma unroll
+        for (int i = 0; i < CE; ++i) t[i] = k + i < K ? src[n * ld + k + i] : (T)0.f;
+        __builtin_memcpy(&v, t, 16);
+      }
+    }
+    *reinterpret_cast<uint4*>(dst + e * CE) = v;
+  }
+}
+
+// Loads of a KTile of R token rows (from n0, multiple of 32) from packed rows.
+template <class T, int R, int BK, int NT>
+struct PackedKLoader {
+  typedef KTile<T, R, BK, NT> Layout;
+  static constexpr int BYTES = Layout::BYTES, NI = Layout::NI, NI_MIN = Layout::NI_MIN;
+  static constexpr bool PARTIAL = Layout::PARTIAL;
+  static constexpr int GROUP = 32 * BK * (int)sizeof(T);  // bytes of one 32-row slice
+  static_assert(R % 32 == 0 && GROUP % 1024 == 0, "whole 32-row groups, whole wave loads");
+  const char* packed;
+  const char* base;
+  int S;
+  uint32_t off[NI];
+  __device__ __forceinline__ void setup(const void* pk, int n0, int s_, int tid = (int)threadIdx.x) {
+    packed = static_cast<const char*>(pk);
+    S = s_;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int lin = i * NT + tid;  // chunk index in the tile image
+      off[i] = (uint32_t)((lin / (32 * Layout::CPR)) * S * GROUP + (lin % (32 * Layout::CPR)) * 16);
+    }
+    rebase(n0);
+  }
+  __device__ __forceinline__ void rebase(int n0) { base = packed + (int64_t)(n0 >> 5) * S * GROUP; }
+  __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
+    if (Layout::PARTIAL && (int)threadIdx.x * 16 >= BYTES) return;  // wave-uniform
+    const rsrc_t r = make_rsrc(base + (int64_t)(k0 / BK) * GROUP);
+    dma_n<NI, NT * 16>(r, off, lds + wave_id() * 1024);
+  }
+};
+
+// Packed size (elements) and slice count of rows [N_pad][K].
+__host__ __device__ __forceinline__ int packed_slices(int64_t K, int bk) {
+  const int64_t s = (K + bk - 1) / bk;
+  return s > 0 ? (int)s : 1;
+}
+
 __device__ __forceinline__ float wave_max32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float wave_sum32(float x) { return x + __shfl_xor(x, 32); }
 

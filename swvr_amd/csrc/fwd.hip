@@ -68,7 +68,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   constexpr int BV = C::BV, BM = C::BM, NT = C::NT;
   constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
   typedef KTile<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile
-  typedef KTile<T, BM, kBK, NT> TB;  // h rows of the token block
+  typedef PackedKLoader<T, BM, kBK, NT> TB;  // h rows of the token block (packed)
   typedef KTile<T, DP, BV, NT> TE;   // E^T tile [DP][BV] in pe_row order, swizzled like an operand tile
   constexpr int SB = TA::BYTES + TB::BYTES;
   constexpr int L = TA::NI_MIN + TB::NI_MIN;  // conservative for partial tiles
@@ -109,7 +109,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   TA ta;
   ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
   TB tbh;
-  tbh.setup(static_cast<const T*>(p.h) + (int64_t)n0 * p.ldh, p.ldh, p.N - n0, p.K);
+  tbh.setup(p.hp, n0, p.hS);
   // issue cursor: the next stage to load (NS - 1 ahead of the compute)
   int is_tile = 0, is_kt = 0, is_slot = 0;
   auto issue_next = [&]() {
@@ -331,6 +331,9 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   pack_et_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
       static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
       const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
+  const int64_t chunks = plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
+  pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
+      static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, const_cast<T*>(static_cast<const T*>(p.hp)));
   timing_end(kKindPack, stream);
   return hipGetLastError();
 }
@@ -382,6 +385,10 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   off += align256((size_t)plan->V_pad * DP * tbytes);
   plan->off_bias = off;
   off += align256((size_t)plan->V_pad * 4);
+  plan->N_pad = ((N + 255) / 256) * 256;
+  plan->hS = packed_slices(K, tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value);
+  plan->off_hp = off;
+  off += align256((size_t)plan->N_pad * plan->hS * (tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value) * tbytes);
   plan->ws_bytes = off;
   return true;
 }
@@ -397,6 +404,8 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
   p.part_acc = reinterpret_cast<float*>(ws + plan.off_acc);
   p.Ep = ws + plan.off_Ep;
   p.biasp = reinterpret_cast<const float*>(ws + plan.off_bias);
+  p.hp = ws + plan.off_hp;
+  p.hS = plan.hS;
   hipError_t e;
   switch (dtype) {
     case kBF16: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, p, stream); break;
