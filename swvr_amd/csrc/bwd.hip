@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__
 // ---------------------------------------------------------------- scores
 struct ScoresParams {
   const void* hp;       // h packed in its tiles' LDS image (pack_rows_kernel)
-  int hS;               // its reduction slices
+  const void* Wp;       // W packed the same way, [V_pad] rows
+  int hS;               // reduction slices of both
   const void* W;
   int64_t ldw;
   const void* Ep;       // packed E [V_pad][DP]
@@ -155,7 +156,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   constexpr int BM = C::BM, BV = C::BV, NT = C::NT;
   constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
   typedef PackedKLoader<T, BM, kBK, NT> TA;  // h rows of the token block (packed)
-  typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
+  typedef PackedKLoader<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile (packed)
   typedef KTile<T, BV, DP, NT> TE;   // E tile
   typedef KTile<T, BM, DP, NT> TG;   // gO tile
   typedef KTile<T, DP, BM, NT> TGT;  // gO^T tile, tokens in pe_row order
@@ -210,7 +211,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   TA ta;
   ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
-  tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
+  tw.setup(p.Wp, vg0, p.hS);
   // issue cursor: the next stage to load (NS - 1 ahead of the compute)
   int is_blk = 0, is_kt = 0, is_slot = 0;
   auto issue_next = [&]() {
@@ -378,7 +379,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   constexpr int BM = C::BM, BV = C::BV, NT = C::NT, NS = C::NS;
   constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
   typedef PackedKLoader<T, BM, kBK, NT> TA;  // h rows of the token block (packed)
-  typedef KTile<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile
+  typedef PackedKLoader<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile (packed)
   typedef KTile<T, BV, DP, NT> TE;   // E tile
   typedef KTile<T, BM, DP, NT> TG;   // gO tile
   typedef KTile<T, DP, BM, NT> TGT;  // gO^T tile, tokens in pe_row order
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   TA ta;
   ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
-  tw.setup(static_cast<const T*>(p.W) + (int64_t)vg0 * p.ldw, p.ldw, rows, p.K);
+  tw.setup(p.Wp, vg0, p.hS);
   const rsrc_t r_none = make_rsrc(nullptr);
   // issue cursor over the walk: stage `issued` is (block is_blk, sub-stage
   // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk, nk+1, nk+2
@@ -950,6 +951,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   T* Ep = reinterpret_cast<T*>(ws + plan.off_Ep);
   float* biasp = reinterpret_cast<float*>(ws + plan.off_bias);
   T* hp = reinterpret_cast<T*>(ws + plan.off_hp);
+  T* Wp = reinterpret_cast<T*>(ws + plan.off_Wp);
 
   {
     const int64_t n = (int64_t)plan.N_pad * plan.DP;
@@ -966,6 +968,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     const int64_t chunks = (int64_t)plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
     pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
         static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, hp);
+    const int64_t wchunks = (int64_t)plan.V_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
+    pack_rows_kernel<T><<<(int)((wchunks + 255) / 256 < 8192 ? (wchunks + 255) / 256 : 8192), 256, 0, stream>>>(
+        static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, wchunks, Wp);
     timing_end(kKindPack, stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
@@ -976,6 +981,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     const int cv = (int)((p.V - v0) < plan.C ? (p.V - v0) : plan.C);
     ScoresParams sp;
     sp.hp = hp;
+    sp.Wp = Wp;
     sp.hS = plan.hS;
     sp.W = p.W;
     sp.ldw = p.ldw;
@@ -1137,6 +1143,8 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->hS = packed_slices(K, bk);
   plan->off_hp = off;
   off += align256((size_t)plan->N_pad * plan->hS * bk * tb);
+  plan->off_Wp = off;
+  off += align256((size_t)plan->V_pad * plan->hS * bk * tb);
   plan->ws_bytes = off;
   return true;
 }

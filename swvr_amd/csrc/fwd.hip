@@ -67,7 +67,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   constexpr int kBK = SliceK<T>::value;
   constexpr int BV = C::BV, BM = C::BM, NT = C::NT;
   constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
-  typedef KTile<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile
+  typedef PackedKLoader<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile (packed)
   typedef PackedKLoader<T, BM, kBK, NT> TB;  // h rows of the token block (packed)
   typedef KTile<T, DP, BV, NT> TE;   // E^T tile [DP][BV] in pe_row order, swizzled like an operand tile
   constexpr int SB = TA::BYTES + TB::BYTES;
@@ -89,7 +89,6 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   const int n0 = tb * BM;
   const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
   const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
-  const T* W = static_cast<const T*>(p.W);
   const T* Ep = static_cast<const T*>(p.Ep);
 
   float m[FT], l[FT];
@@ -107,7 +106,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsE = lds0 + NS * SB, ldsB = ldsE + EBYTES;
   TA ta;
-  ta.setup(W + (int64_t)vt_begin * BV * p.ldw, p.ldw, p.V - vt_begin * BV, p.K);
+  ta.setup(p.Wp, vt_begin * BV, p.hS);
   TB tbh;
   tbh.setup(p.hp, n0, p.hS);
   // issue cursor: the next stage to load (NS - 1 ahead of the compute)
@@ -116,7 +115,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
     if (is_tile >= n_tiles) return;
     if (is_kt == 0) {
       const int v0 = (vt_begin + is_tile) * BV;
-      ta.rebase(W + (int64_t)v0 * p.ldw, p.V - v0);
+      ta.rebase(v0);
     }
     const uint32_t st = lds0 + is_slot * SB;
     ta.issue(st, is_kt * kBK);
@@ -334,6 +333,9 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   const int64_t chunks = plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
   pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
       static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, const_cast<T*>(static_cast<const T*>(p.hp)));
+  const int64_t wchunks = (int64_t)plan.V_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
+  pack_rows_kernel<T><<<(int)((wchunks + 255) / 256 < 8192 ? (wchunks + 255) / 256 : 8192), 256, 0, stream>>>(
+      static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, wchunks, const_cast<T*>(static_cast<const T*>(p.Wp)));
   timing_end(kKindPack, stream);
   return hipGetLastError();
 }
@@ -389,6 +391,8 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   plan->hS = packed_slices(K, tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value);
   plan->off_hp = off;
   off += align256((size_t)plan->N_pad * plan->hS * (tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value) * tbytes);
+  plan->off_Wp = off;
+  off += align256((size_t)plan->V_pad * plan->hS * (tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value) * tbytes);
   plan->ws_bytes = off;
   return true;
 }
@@ -405,6 +409,7 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
   p.Ep = ws + plan.off_Ep;
   p.biasp = reinterpret_cast<const float*>(ws + plan.off_bias);
   p.hp = ws + plan.off_hp;
+  p.Wp = ws + plan.off_Wp;
   p.hS = plan.hS;
   hipError_t e;
   switch (dtype) {

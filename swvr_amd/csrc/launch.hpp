@@ -41,7 +41,8 @@ struct FwdParams {
   const void* Ep;      // packed E^T tiles [n_vt][DP][BV], compute dtype
   const float* biasp;  // packed bias [V_pad], -inf past V
   const void* hp;      // h packed in its tiles' LDS image (pack_rows_kernel)
-  int hS;              // its reduction slices
+  const void* Wp;      // W packed the same way, [V_pad] rows
+  int hS;              // reduction slices of both
 };
 
 struct FwdPlan {
@@ -49,8 +50,8 @@ struct FwdPlan {
   int n_tb, n_vt, n_split, n_part;
   int V_pad;
   int64_t N_pad;         // token rows of the packed h
-  int hS;                // reduction slices of the packed h
-  size_t off_m, off_l, off_acc, off_Ep, off_bias, off_hp, ws_bytes;
+  int hS;                // reduction slices of the packed h and W
+  size_t off_m, off_l, off_acc, off_Ep, off_bias, off_hp, off_Wp, ws_bytes;
 };
 
 // Tile shape, split count and workspace for a forward call; ok=false if the
@@ -72,8 +73,8 @@ struct BwdPlan {
   int n_gpart;           // dE / db partials per chunk
   bool dh_acc;           // dh needs an fp32 accumulator across chunks
   int V_pad;             // vocabulary rows of the packed E / bias
-  int hS;                // reduction slices of the packed h
-  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, ws_bytes;
+  int hS;                // reduction slices of the packed h and W
+  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, off_Wp, ws_bytes;
 };
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
