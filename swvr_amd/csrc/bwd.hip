@@ -668,12 +668,14 @@ struct StageKLoader {
   }
 };
 
-// dh, A: rows = positions from q0 (multiple of 32), k = vocabulary rows.
-// Every vocabulary row a slice reaches (below the chunk's rows rounded up to
-// the scores tile) holds dS, zero past the chunk, so no bounds apply.
+// dh, A: rows = positions from q0 (multiple of 32), k = vocabulary rows,
+// staged block-major (BRTile): a slice is R / 32 consecutive stage blocks, one
+// contiguous run.  Every vocabulary row a slice reaches (below the chunk's
+// rows rounded up to the scores tile) holds dS, zero past the chunk, so no
+// bounds apply.
 template <class T, int R, int BK, int NT>
-struct StageRLoader {
-  typedef RTile<T, R, BK, NT> Layout;
+struct StageBRLoader {
+  typedef BRTile<T, R, BK, NT> Layout;
   static constexpr int BYTES = Layout::BYTES, NI = Layout::NI, NI_MIN = Layout::NI_MIN;
   static_assert(32 % BK == 0, "slices inside a block");
   const char* base;
@@ -684,10 +686,8 @@ struct StageRLoader {
     base = static_cast<const char*>(stage) + stage_off(0, q0, ntb) * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int lin = (i * NT + (int)threadIdx.x) * 16;
-      const int kr = lin / Layout::ROWB;
-      const int r = (((lin % Layout::ROWB) / 16) ^ Layout::swz(kr)) * Layout::CE;
-      off[i] = (uint32_t)(stage_off(kr, r, ntb) * (int)sizeof(T));
+      const int lin = (i * NT + (int)threadIdx.x) * 16;  // byte in the tile image
+      off[i] = (uint32_t)((lin / Layout::SUB) * 1024 * (int)sizeof(T) + lin % Layout::SUB);
     }
   }
   __device__ __forceinline__ void issue(uint32_t lds, int k0) const {
@@ -800,7 +800,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
     // whole 32-position blocks: a partial block's tokens sit anywhere in it
     gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (p.N + 31) & ~31, wm * (GM / G::WM), wn * (GN / G::WN));
   } else {
-    StageRLoader<T, GM, kBK, NT> ta;
+    StageBRLoader<T, GM, kBK, NT> ta;
     ta.setup(p.stage, mt * GM, p.n_tb32);
     RTile<T, GN, kBK, NT> tb;
     tb.setup(static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);

@@ -524,6 +524,65 @@ struct OpOffsets<RTile<T, R, BK, NT>, F, J> {
   }
 };
 
+// Block-major transposed tile: the rows of the operand come in groups of 32,
+// each group a [BK k-rows][32 rows] sub-tile of its own (the image of one
+// 32 x 32 block of a block-tiled source, copied as one contiguous run).  The
+// operand reads transpose like RTile's; within a sub-tile a k-row is 64
+// bytes (bf16), so the 4 k-rows x 32 bytes that a 16-lane group of a
+// transposing read touches fall on 32 distinct banks without any swizzle.
+template <class T, int R, int BK, int NT>
+struct BRTile {
+  typedef BRTile Layout;
+  static constexpr int CE = 16 / (int)sizeof(T);
+  static constexpr int KROWB = 32 * (int)sizeof(T);  // bytes of one k-row of a sub-tile
+  static constexpr int SUB = BK * KROWB;             // bytes of one 32-row sub-tile
+  static constexpr int BYTES = R / 32 * SUB;
+  static constexpr int NI = BYTES / (NT * 16);
+  static constexpr int NI_MIN = NI;
+  static_assert(R % 32 == 0 && BYTES % (NT * 16) == 0, "whole sub-tiles, whole workgroup loads");
+};
+
+template <class T, int R, int BK, int NT, int F, int J>
+struct OpOffsets<BRTile<T, R, BK, NT>, F, J> {
+  typedef BRTile<T, R, BK, NT> BT;
+  typedef typename Vec8<T>::type V8;
+  uint32_t off[F];
+  __device__ __forceinline__ void init(int row0) {
+    const int lane = lane_id();
+    if constexpr (sizeof(T) == 2) {
+      // lane = 32 hi + 16 g + 4 a + q reads k-row 8 hi + a (+ 16 j + 4 h) at
+      // rows 16 g + 4 q .. + 3 of sub-tile (row0 + 32 f) / 32
+      const int hi = lane >> 5, g = (lane >> 4) & 1, a = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+      for (int f = 0; f < F; ++f)
+        off[f] = (uint32_t)(((row0 + 32 * f) >> 5) * BT::SUB + (8 * hi + a) * BT::KROWB + (16 * g + 4 * q) * 2);
+    } else {
+      // this lane's row (lane % 32) and first k-row (8 (lane / 32))
+#pragma unroll
+      for (int f = 0; f < F; ++f)
+        off[f] = (uint32_t)(((row0 + 32 * f) >> 5) * BT::SUB + 8 * (lane >> 5) * BT::KROWB + (lane & 31) * 4);
+    }
+  }
+  __device__ __forceinline__ V8 read(const char* stage, int j, int f) const {
+    if constexpr (sizeof(T) == 2) {
+      const char* p = stage + off[f] + j * 16 * BT::KROWB;
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+      const s16x4_t hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p + 4 * BT::KROWB));
+      const s16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      V8 out;
+      __builtin_memcpy(&out, &both, 16);
+      return out;
+    } else {
+      V8 out;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        out[t] = *reinterpret_cast<const float*>(stage + off[f] + (16 * j + t) * BT::KROWB);
+      return out;
+    }
+  }
+};
+
 // MFMA operands of one k16 step of a wave's FM x FN grid of 32x32 blocks.
 template <class T, int FM, int FN>
 struct StepOps {
