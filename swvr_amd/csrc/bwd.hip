@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__
 
 // ---------------------------------------------------------------- scores
 struct ScoresParams {
-  const void* hp;       // h packed in its tiles' LDS image (pack_rows_kernel)
+  const void* hp;       // h packed in its tiles' LDS image (pack_rows_tiled_kernel)
   const void* Wp;       // W packed the same way, [V_pad] rows
   int hS;               // reduction slices of both
   const void* W;
@@ -965,14 +965,14 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     timing_begin(kKindPack, stream);
     pack_vocab_kernel<T><<<(int)((nv + 255) / 256), 256, 0, stream>>>(
         static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp);
-    const int64_t chunks = (int64_t)plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
-    pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
-        static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, hp);
-    const int64_t wchunks = (int64_t)plan.V_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
-    pack_rows_kernel<T><<<(int)((wchunks + 255) / 256 < 8192 ? (wchunks + 255) / 256 : 8192), 256, 0, stream>>>(
-        static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, wchunks, Wp);
-    timing_end(kKindPack, stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_pack_rows<T>(static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, plan.N_pad, hp, stream)) !=
+        hipSuccess)
+      return e;
+    if ((e = launch_pack_rows<T>(static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream)) !=
+        hipSuccess)
+      return e;
+    timing_end(kKindPack, stream);
   }
 
   const bool need_stage = p.gh || p.gW;

@@ -752,32 +752,48 @@ struct CountedRing {
 // XOR-swizzled place (KTile layout), zeros past N and K.  A tile of any
 // multiple of 32 rows then loads a reduction slice as contiguous 2 KB runs
 // (full cache lines instead of one 64-byte piece per row) with no bounds.
+// One workgroup per 32 rows x 8 slices: the rows are read as contiguous
+// 512-byte runs into LDS, the 8 slices written as one contiguous 16 KB run.
 template <class T>
-__global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ src, int64_t ld, int N, int K, int S,
-                                                        int64_t n_chunks, T* __restrict__ dst) {
+__global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const T* __restrict__ src, int64_t ld, int N, int K,
+                                                              int S, T* __restrict__ dst) {
   constexpr int BK = SliceK<T>::value, CE = 16 / (int)sizeof(T), CPR = BK / CE;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_chunks;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t per_group = (int64_t)S * 32 * CPR;
-    const int64_t grp = e / per_group;
-    const int rem = (int)(e - grp * per_group);
-    const int s = rem / (32 * CPR), lin = rem % (32 * CPR);
-    const int row = lin / CPR, pc = lin % CPR;
-    const int64_t n = grp * 32 + row;
-    const int k = s * BK + (pc ^ chunk_swizzle(row, CPR)) * CE;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (n < N) {
-      if (k + CE <= K) {
-        v = *reinterpret_cast<const uint4*>(src + n * ld + k);
-      } else if (k < K) {
-        T t[CE];
+  static_assert(CPR == 4, "4 chunks per slice row");
+  constexpr int SPW = 8;                    // slices per workgroup
+  constexpr int RSTRIDE = SPW * CPR + 1;    // chunks per LDS row (one pad chunk: no bank conflicts)
+  __shared__ uint4 tile[32 * RSTRIDE];
+  const int SG = (S + SPW - 1) / SPW;
+  const int grp = blockIdx.x / SG, s0 = (blockIdx.x % SG) * SPW;
+  const int ns = S - s0 < SPW ? S - s0 : SPW;
+  const int t = threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < CE; ++i) t[i] = k + i < K ? src[n * ld + k + i] : (T)0.f;
-        __builtin_memcpy(&v, t, 16);
-      }
-    }
-    *reinterpret_cast<uint4*>(dst + e * CE) = v;
+  for (int i = 0; i < 4; ++i) {
+    const int row = i * 8 + t / 32, kc = t % 32;
+    const int64_t n = (int64_t)grp * 32 + row;
+    const int k = (s0 * CPR + kc) * CE;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (kc < ns * CPR && n < N && k < K) v = *reinterpret_cast<const uint4*>(src + n * ld + k);
+    tile[row * RSTRIDE + kc] = v;
   }
+  __syncthreads();
+  T* out = dst + ((int64_t)grp * S + s0) * 32 * BK;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int o = i * 256 + t;
+    const int sl = o / (32 * CPR), r = (o / CPR) % 32, pc = o % CPR;
+    if (sl < ns)
+      reinterpret_cast<uint4*>(out)[o] = tile[r * RSTRIDE + sl * CPR + (pc ^ chunk_swizzle(r, CPR))];
+  }
+}
+
+// Pack rows [rows_pad][K] of src (rows_pad a multiple of 32) into the tile image.
+template <class T>
+__host__ hipError_t launch_pack_rows(const T* src, int64_t ld, int N, int K, int S, int64_t rows_pad, T* dst,
+                                     hipStream_t stream) {
+  const int64_t blocks = (rows_pad / 32) * ((S + 7) / 8);
+  if (blocks == 0) return hipSuccess;
+  pack_rows_tiled_kernel<T><<<(unsigned)blocks, 256, 0, stream>>>(src, ld, N, K, S, dst);
+  return hipGetLastError();
 }
 
 // Loads of a KTile of R token rows (from n0, multiple of 32) from packed rows.

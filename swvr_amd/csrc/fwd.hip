@@ -330,14 +330,15 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   pack_et_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
       static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
       const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
-  const int64_t chunks = plan.N_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
-  pack_rows_kernel<T><<<(int)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192), 256, 0, stream>>>(
-      static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, chunks, const_cast<T*>(static_cast<const T*>(p.hp)));
-  const int64_t wchunks = (int64_t)plan.V_pad * plan.hS * SliceK<T>::value / (16 / (int)sizeof(T));
-  pack_rows_kernel<T><<<(int)((wchunks + 255) / 256 < 8192 ? (wchunks + 255) / 256 : 8192), 256, 0, stream>>>(
-      static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, wchunks, const_cast<T*>(static_cast<const T*>(p.Wp)));
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = launch_pack_rows<T>(static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, plan.N_pad,
+                            const_cast<T*>(static_cast<const T*>(p.hp)), stream);
+  if (e == hipSuccess)
+    e = launch_pack_rows<T>(static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, plan.V_pad,
+                            const_cast<T*>(static_cast<const T*>(p.Wp)), stream);
   timing_end(kKindPack, stream);
-  return hipGetLastError();
+  return e;
 }
 
 }  // namespace

@@ -40,7 +40,7 @@ struct FwdParams {
   float* part_acc;     // [n_part][DP][N]
   const void* Ep;      // packed E^T tiles [n_vt][DP][BV], compute dtype
   const float* biasp;  // packed bias [V_pad], -inf past V
-  const void* hp;      // h packed in its tiles' LDS image (pack_rows_kernel)
+  const void* hp;      // h packed in its tiles' LDS image (pack_rows_tiled_kernel)
   const void* Wp;      // W packed the same way, [V_pad] rows
   int hS;              // reduction slices of both
 };
