@@ -607,38 +607,73 @@ struct GemmParams {
   float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
 };
 
-// Write a GEMM accumulator tile: out[(row_off + row) * ld + col] = scale * acc (+ prev[...]),
-// rows < rows, cols < ld.  prev (fp32, may alias out) is added when non-null.
-// prev may alias out (the running fp32 dh): the previous values of a row of
-// blocks are all loaded before any of them is overwritten, so the loads do not
-// wait for one store after another.
-// POS: the tile's rows are stage positions (row0 multiple of 32), written to
-// their tokens.
-template <int FM, int FN, bool POS = false, class OutT>
+// Store 4 fp32 values as OutT (one 16- or 8-byte store).
+template <class OutT>
+__device__ __forceinline__ void store4(OutT* dst, float4 v) {
+  if constexpr (sizeof(OutT) == 4) {
+    *reinterpret_cast<float4*>(dst) = v;
+  } else {
+    OutT q[4] = {from_float<OutT>(v.x), from_float<OutT>(v.y), from_float<OutT>(v.z), from_float<OutT>(v.w)};
+    uint2 u;
+    __builtin_memcpy(&u, q, 8);
+    *reinterpret_cast<uint2*>(dst) = u;
+  }
+}
+
+// Write a GEMM tile through LDS: out[(row_off + row) * ld + col] = scale * acc
+// (+ prev[...]) for rows < rows, cols < ld, with the tile at (tile_row0,
+// tile_col0).  A lane's accumulators hold one column and 16 rows, so direct
+// stores would be 2- or 4-byte pieces; instead each half of the tile (the
+// rows of one wave row) is laid out row-major in LDS and written back by all
+// threads as 16-byte chunks of whole rows.  prev (fp32, may alias out) is
+// read per chunk just before the chunk is overwritten.  POS: the tile's rows
+// are stage positions (tile_row0 multiple of 32), written to their tokens.
+template <class G, int FM, int FN, bool POS = false, class OutT>
 __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float scale, OutT* out,
-                                           const float* prev, int64_t row_off, int rows, int row0, int col0,
-                                           int ld) {
-  const int lane = lane_id();
+                                           const float* prev, int64_t row_off, int rows, int tile_row0,
+                                           int tile_col0, int ld, char* smem) {
+  constexpr int HALF = G::GM / G::WM, LSTR = G::GN + 8;  // rows per pass, floats per LDS row
+  static_assert(HALF * LSTR * 4 <= G::EPI_BYTES, "epilogue fits in LDS");
+  float* lds = reinterpret_cast<float*>(smem);
+  const int lane = lane_id(), w = wave_id(), wm = w / G::WN, wn = w % G::WN;
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    float pv[FN][16];
+  for (int pass = 0; pass < G::WM; ++pass) {
+    __syncthreads();  // every wave is done with the LDS (operand ring, or the previous pass)
+    if (wm == pass) {
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const int col = col0 + fn * 32 + (lane & 31);
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = row0 + fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
-        pv[fn][r] = (prev && row < rows && col < ld) ? prev[(row_off + row) * ld + col] : 0.f;
-      }
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rl = fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
+            lds[rl * LSTR + wn * (G::GN / G::WN) + fn * 32 + (lane & 31)] = acc[fm][fn][r] * scale;
+          }
+    }
+    __syncthreads();
+    // every chunk's previous value is requested before any is used, so the
+    // read-modify-write costs one memory round trip per pass
+    constexpr int CPRW = G::GN / 4;               // 16-byte chunks per row
+    constexpr int ITER = HALF * CPRW / G::NT;     // chunks per thread
+    static_assert(HALF * CPRW % G::NT == 0, "whole chunks per thread");
+    float4 pv[ITER];
+    int64_t off[ITER];
+    bool ok[ITER];
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int c = i * G::NT + (int)threadIdx.x;
+      const int rr = c / CPRW, c4 = c % CPRW;
+      const int row = tile_row0 + pass * HALF + rr, col = tile_col0 + c4 * 4;
+      ok[i] = row < rows && col < ld;  // ld is a multiple of 8: a chunk is wholly in or out
+      off[i] = (row_off + row) * ld + col;
+      pv[i] = (prev && ok[i]) ? *reinterpret_cast<const float4*>(prev + off[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const int col = col0 + fn * 32 + (lane & 31);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = row0 + fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
-        if (row < rows && col < ld) out[(row_off + row) * ld + col] = (OutT)fmaf(acc[fm][fn][r], scale, pv[fn][r]);
-      }
+    for (int i = 0; i < ITER; ++i) {
+      const int c = i * G::NT + (int)threadIdx.x;
+      float4 v = *reinterpret_cast<const float4*>(lds + (c / CPRW) * LSTR + (c % CPRW) * 4);
+      v.x += pv[i].x; v.y += pv[i].y; v.z += pv[i].z; v.w += pv[i].w;
+      if (ok[i]) store4(out + off[i], v);
     }
   }
 }
@@ -772,6 +807,11 @@ struct GemmTile {
   static constexpr int WM = 2;
   static constexpr int WN = wide ? 4 : 2;
   static constexpr int NT = 64 * WM * WN;
+  // LDS: the operand ring, then (reused) the row-major epilogue staging of
+  // half a tile in fp32 (rows padded by 8 floats: conflict-free writes)
+  static constexpr int RING_BYTES = kStages * 2 * GM * SliceK<T>::value * (int)sizeof(T);
+  static constexpr int EPI_BYTES = GM / WM * (GN + 8) * 4;
+  static constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
 };
 
 // One tile of one gradient product; DW selects the product (q: stage
@@ -807,26 +847,25 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
     gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / G::WM), wn * (GN / G::WN));
   }
   const int rows = DW ? p.cv : p.N;
-  const int row0 = mt * GM + wm * (GM / G::WM);
-  const int col0 = nt * GN + wn * (GN / G::WN);
+  const int row0 = mt * GM, col0 = nt * GN;
   // dispatch on the output dtype outside the unrolled store loops
   if constexpr (DW) {
     if (p.gW_dtype == kBF16)
-      gemm_store<FM, FN>(acc, p.scale, static_cast<bf16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<G>(acc, p.scale, static_cast<bf16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K, smem);
     else if (p.gW_dtype == kF16)
-      gemm_store<FM, FN>(acc, p.scale, static_cast<f16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<G>(acc, p.scale, static_cast<f16_t*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K, smem);
     else
-      gemm_store<FM, FN>(acc, p.scale, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K);
+      gemm_store<G>(acc, p.scale, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K, smem);
   } else {
     const float* prev = p.dh_first ? nullptr : p.dh_acc;
     if (!p.dh_last)
-      gemm_store<FM, FN, true>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K);
+      gemm_store<G, FM, FN, true>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K, smem);
     else if (p.gh_dtype == kBF16)
-      gemm_store<FM, FN, true>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
     else if (p.gh_dtype == kF16)
-      gemm_store<FM, FN, true>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
     else
-      gemm_store<FM, FN, true>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K);
+      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
   }
 }
 
@@ -840,7 +879,8 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   constexpr int SB = KTile<T, G::GM, kBK, G::NT>::BYTES + RTile<T, G::GN, kBK, G::NT>::BYTES;
   static_assert(KTile<T, G::GM, kBK, G::NT>::BYTES == RTile<T, G::GM, kBK, G::NT>::BYTES,
                 "both A layouts stage the same bytes");
-  __shared__ __attribute__((aligned(1024))) char smem[kStages * SB];
+  static_assert(kStages * SB <= G::LDS_BYTES, "ring fits");
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
   const int b = blockIdx.x;
   if (b < p.n_dw)
     gemm_tile<T, true>(p, xcd_swizzle(b, p.n_dw), smem);
