@@ -106,8 +106,9 @@ __host__ __device__ __forceinline__ int64_t stage_off(int v, int q, int n_tb32) 
 // One 32 x 32 accumulator block of dS (lane column: vocabulary row vc,
 // registers: the block's 32 tokens from tok0) into the stage.
 template <class T>
-__device__ __forceinline__ void store_ds_block(const f32x16_t& ds, void* stage, int n_tb32, int vc, int tok0) {
-  T* dst = static_cast<T*>(stage) + stage_off(vc, tok0, n_tb32) + (lane_id() >> 5) * 16;
+__device__ __forceinline__ void store_ds_block(const f32x16_t& ds, void* stage, int n_tb32, int vc, int tok0,
+                                               int lane = lane_id()) {
+  T* dst = static_cast<T*>(stage) + stage_off(vc, tok0, n_tb32) + (lane >> 5) * 16;
   if constexpr (sizeof(T) == 2) {
     T q[16];
 #pragma unroll
@@ -441,7 +442,8 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
       if (is_sub == 0) {
         ta.rebase(n0);
         // LSE and delta of the block into strip (block & 1), ahead of its slices
-        const int c = threadIdx.x;
+        // (offsets recomputed per block, see opaque_zero)
+        const int c = (int)threadIdx.x + opaque_zero();
         if (c < BM / 2) {
           const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
           dma_batch1(make_rsrc(p.lsed), off, ldsL + (is_blk & 1) * (2 * BM * 4) + w * 1024);
@@ -504,28 +506,32 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
     TE tel;
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv) {
-      const int vl = wv * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
-        // LDS bases recomputed per block (see opaque_zero): the side tiles sit
-        // in the three slots before and at the current one
-        const int oz = opaque_zero();
-        const char* sGte = smem + oz + slot_gt * SB;
-        const char* sGe = smem + oz + ((slot_gt + NS - 1) % NS) * SB;
-        const char* sEe = smem + oz + ((slot_gt + NS - 2) % NS) * SB;
-        const float* sLe = sLD + oz + (blk & 1) * (2 * BM);
+        // Every lane-dependent offset below derives from an opaque copy of the
+        // lane's row (see opaque_zero), so it is recomputed here, per block:
+        // hoisted out of the block loop they would be spilled, and each reload
+        // from scratch waits (vmcnt in order) for every store issued before it.
+        const int ln = lane + opaque_zero();
+        const int lr = ln & 31;
+        const int vl = wv * WVR + fv * 32 + lr;  // tile-local row of this lane
+        // the side tiles sit in the three slots before and at the current one
+        const char* sGte = smem + slot_gt * SB;
+        const char* sGe = smem + ((slot_gt + NS - 1) % NS) * SB;
+        const char* sEe = smem + ((slot_gt + NS - 2) % NS) * SB;
+        const float* sLe = sLD + (blk & 1) * (2 * BM);
         const float* sDe = sLe + BM;
         const int tr0 = wt * WTR + ft * 32;  // first token of the block
         // dP block = gO[tokens] E[rows]^T over D
         f32x16_t dp = zero16();
 #pragma unroll
         for (int kd = 0; kd < DK; ++kd)
-          mfma_k16(dp, read_op(tgl, sGe, tr0 + (lane & 31), kd), read_op(tel, sEe, vl, kd));
+          mfma_k16(dp, read_op(tgl, sGe, tr0 + lr, kd, ln), read_op(tel, sEe, vl, kd, ln));
         float dbs = 0.f;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
-          const int tl = tr0 + 8 * g4 + (lane >> 5) * 4;
+          const int tl = tr0 + 8 * g4 + (ln >> 5) * 4;
           const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
           const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
           const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
           }
         }
         dbacc[fv] += dbs;
-        if (p.need_stage) store_ds_block<T>(dp, p.stage, p.n_tb32, vl0 + vl, n0 + tr0);
+        if (p.need_stage) store_ds_block<T>(dp, p.stage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
         if (p.need_dE) {
           // dE^T[d][v] += gO^T[d][tok] P[tok][v]; registers 8c..8c+7 hold
           // tokens 16c + 8(t/4) + 4(lane/32) + t%4, stored contiguously in
@@ -550,10 +556,10 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
             V8 bv;
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[ft][fv][8 * c + tt]);
-            const int p0 = tr0 + 8 * (2 * c + (lane >> 5));
+            const int p0 = tr0 + 8 * (2 * c + (ln >> 5));
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-              const V8 av = *reinterpret_cast<const V8*>(sGte + TGT::elem(db * 32 + (lane & 31), p0));
+              const V8 av = *reinterpret_cast<const V8*>(sGte + TGT::elem(db * 32 + lr, p0));
               mfma_k16(deacc[db][fv], av, bv);
             }
           }

@@ -374,13 +374,13 @@ struct RTile {
   }
 };
 
-// MFMA operand (8 reduction values of one row) from a staged tile.
+// MFMA operand (8 reduction values of one row) from a staged tile.  `lane`
+// is this lane's index (an epilogue passes an opaque copy, see opaque_zero).
 template <class T, int R, int BK, int NT>
 __device__ __forceinline__ typename Vec8<T>::type read_op(const KTile<T, R, BK, NT>&, const char* stage, int row,
-                                                          int j) {
+                                                          int j, int lane = lane_id()) {
   typedef KTile<T, R, BK, NT> KT;
   typedef typename Vec8<T>::type V8;
-  const int lane = lane_id();
   const int k = 16 * j + (lane >> 5) * 8;
   const int c = k / KT::CE;
   const char* rowp = stage + row * KT::ROWB;
