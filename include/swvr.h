@@ -21,7 +21,7 @@
  *  - Row-major operands with unit stride in the last dimension.  h, W and E
  *    have row strides ldh, ldw, lde (in elements).  K, ldh and ldw must be
  *    multiples of 8 and h, W 16-byte aligned (the host pads odd K with zero
- *    columns).  D and lde are unrestricted.
+ *    columns); K is at most 2^21.  D and lde are unrestricted.
  *  - The operand dtype (SWVR_BF16, SWVR_F16, SWVR_F32) is the compute dtype of
  *    the matrix products: the reference's `cdt` (swvr/api.py:8-11).  Products
  *    accumulate in fp32; scores, softmax state, O and LSE are fp32.

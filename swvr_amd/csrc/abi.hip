@@ -69,6 +69,8 @@ int check_common(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const vo
     return fail(SWVR_EDTYPE, "D=%lld exceeds the maximum %lld for this dtype", (long long)D,
                 (long long)swvr_max_d(dtype));
   if (K % 8 != 0) return fail(SWVR_EINVAL, "K=%lld must be a multiple of 8 (pad h and W)", (long long)K);
+  // tile-relative byte offsets of the kernels are 32-bit: 128 rows x K fp32 stay below 2^31
+  if (K > (int64_t)1 << 21) return fail(SWVR_EINVAL, "K=%lld exceeds the maximum %lld", (long long)K, 1LL << 21);
   if (ldh < K || ldh % 8 != 0) return fail(SWVR_EINVAL, "ldh=%lld must be >= K and a multiple of 8", (long long)ldh);
   if (ldw < K || ldw % 8 != 0) return fail(SWVR_EINVAL, "ldw=%lld must be >= K and a multiple of 8", (long long)ldw);
   if (lde < D) return fail(SWVR_EINVAL, "lde=%lld must be >= D", (long long)lde);

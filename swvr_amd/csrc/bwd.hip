@@ -613,6 +613,23 @@ struct GemmParams {
   float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
 };
 
+// Store 4 fp32 values as OutT (one 16- or 8-byte buffer store at byte offset
+// voff of r; kOOB drops it).
+template <class OutT>
+__device__ __forceinline__ void store4_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, float4 v) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  if constexpr (sizeof(OutT) == 4) {
+    const u32x4 u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(u, r, (int)voff, 0, 0);
+  } else {
+    OutT q[4] = {from_float<OutT>(v.x), from_float<OutT>(v.y), from_float<OutT>(v.z), from_float<OutT>(v.w)};
+    u32x2 u;
+    __builtin_memcpy(&u, q, 8);
+    __builtin_amdgcn_raw_buffer_store_b64(u, r, (int)voff, 0, 0);
+  }
+}
+
 // Store 4 fp32 values as OutT (one 16- or 8-byte store).
 template <class OutT>
 __device__ __forceinline__ void store4(OutT* dst, float4 v) {
@@ -657,29 +674,36 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float 
           }
     }
     __syncthreads();
-    // every chunk's previous value is requested before any is used, so the
-    // read-modify-write costs one memory round trip per pass
+    // Every chunk's previous value is requested before any is used, so the
+    // read-modify-write costs one memory round trip per pass.  Loads and
+    // stores are buffer operations with out-of-range chunks masked by offset,
+    // not by branches: around divergent branches the compiler cannot count
+    // the outstanding operations and waits for all of them before every add,
+    // which would serialise the stores.
     constexpr int CPRW = G::GN / 4;               // 16-byte chunks per row
     constexpr int ITER = HALF * CPRW / G::NT;     // chunks per thread
     static_assert(HALF * CPRW % G::NT == 0, "whole chunks per thread");
+    const int64_t first = (row_off + tile_row0 + pass * HALF) * ld + tile_col0;  // element of the pass's corner
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(prev ? prev + first : nullptr);  // null prev: loads read zeros
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out + first);
     float4 pv[ITER];
-    int64_t off[ITER];
-    bool ok[ITER];
+    uint32_t el[ITER];  // element offset from the corner, or kOOB
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int c = i * G::NT + (int)threadIdx.x;
       const int rr = c / CPRW, c4 = c % CPRW;
       const int row = tile_row0 + pass * HALF + rr, col = tile_col0 + c4 * 4;
-      ok[i] = row < rows && col < ld;  // ld is a multiple of 8: a chunk is wholly in or out
-      off[i] = (row_off + row) * ld + col;
-      pv[i] = (prev && ok[i]) ? *reinterpret_cast<const float4*>(prev + off[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // ld is a multiple of 8: a chunk is wholly in or out
+      el[i] = row < rows && col < ld ? (uint32_t)(rr * ld + c4 * 4) : kOOB;
+      const uint32_t vo = el[i] == kOOB ? kOOB : el[i] * 4;
+      pv[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rp, (int)vo, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int c = i * G::NT + (int)threadIdx.x;
       float4 v = *reinterpret_cast<const float4*>(lds + (c / CPRW) * LSTR + (c % CPRW) * 4);
       v.x += pv[i].x; v.y += pv[i].y; v.z += pv[i].z; v.w += pv[i].w;
-      if (ok[i]) store4(out + off[i], v);
+      store4_buf<OutT>(ro, el[i] == kOOB ? kOOB : el[i] * (uint32_t)sizeof(OutT), v);
     }
   }
 }

@@ -139,6 +139,17 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
   return r;
 }
 
+// The same descriptor as the compiler's buffer resource type, for the buffer
+// load / store builtins (whose memory operations the compiler counts, unlike
+// inline asm).  A load at offset kOOB returns zeros; a store there is dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t ua = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(ua), (short)0, base ? 0x7FFFFFFF : 0,
+                                           0x00020000);
+}
+
 // Wave-uniform LDS byte address of a pointer into __shared__ memory.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const char*)p);

@@ -70,6 +70,7 @@ def call_fwd(dtype=_lib.BF16, N=4, K=16, V=8, D=4, h=16, ldh=16, W=16, ldw=16, E
     (dict(D=300, lde=300), _lib.EDTYPE),            # D above the bf16 cap
     (dict(dtype=_lib.F32, D=200, lde=200), _lib.EDTYPE),
     (dict(N=-1), _lib.EINVAL),
+    (dict(K=(1 << 21) + 8, ldh=(1 << 21) + 8, ldw=(1 << 21) + 8), _lib.EINVAL),  # K above the 32-bit offset cap
 ])
 def test_abi_rejects_bad_arguments_without_touching_the_device(kw, code):
     assert call_fwd(**kw) == code
