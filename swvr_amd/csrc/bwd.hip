@@ -108,19 +108,25 @@ __host__ __device__ __forceinline__ int64_t stage_off(int v, int q, int n_tb32) 
 template <class T>
 __device__ __forceinline__ void store_ds_block(const f32x16_t& ds, void* stage, int n_tb32, int vc, int tok0,
                                                int lane = lane_id()) {
-  T* dst = static_cast<T*>(stage) + stage_off(vc, tok0, n_tb32) + (lane >> 5) * 16;
+  // Non-temporal stores: the stage is read back by the next launch, not by
+  // this one, so its lines need not displace the operand slices in L2.
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4* dst = reinterpret_cast<u32x4*>(static_cast<T*>(stage) + stage_off(vc, tok0, n_tb32) + (lane >> 5) * 16);
   if constexpr (sizeof(T) == 2) {
     T q[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) q[r] = from_float<T>(ds[r]);
-    uint4 u[2];
+    u32x4 u[2];
     __builtin_memcpy(u, q, 32);
-    reinterpret_cast<uint4*>(dst)[0] = u[0];
-    reinterpret_cast<uint4*>(dst)[1] = u[1];
+    __builtin_nontemporal_store(u[0], dst);
+    __builtin_nontemporal_store(u[1], dst + 1);
   } else {
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      reinterpret_cast<float4*>(dst)[g] = make_float4(ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]);
+    for (int g = 0; g < 4; ++g) {
+      const u32x4 u = {__float_as_uint(ds[4 * g]), __float_as_uint(ds[4 * g + 1]), __float_as_uint(ds[4 * g + 2]),
+                       __float_as_uint(ds[4 * g + 3])};
+      __builtin_nontemporal_store(u, dst + g);
+    }
   }
 }
 
