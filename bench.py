@@ -9,7 +9,10 @@ A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
 Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd TFLOP/s,
 2 N V (4K + 3D) / step time — the FLOPs of the reference's algorithm with one
-score recompute (docs/DESIGN.md:39); ``ms_per_step`` is the step time.
+score recompute (docs/DESIGN.md:39); ``ms_per_step`` is the step time.  The
+backward skips tokens whose cotangents are all zero (weight 0 in the loss):
+``bwd_active_tokens`` says how many it ran over, ``work_tflops`` counts only
+the FLOPs done, and the per-kernel rates and the roofline are priced on them.
 
 The dominant kernel's roofline is measured live: every launch in the timed
 region is bracketed by HIP events on its own stream (the C ABI's timing
@@ -75,14 +78,19 @@ def algorithmic_flops(N, K, V, D):
     return fwd, 2.0 * N * V * (4 * K + 3 * D)
 
 
-def kernel_flops(name, N, K, V, D):
-    """Algorithmic FLOPs of all launches of one kernel kind over one step."""
+def kernel_flops(name, N, K, V, D, n_act=None):
+    """Algorithmic FLOPs of all launches of one kernel kind over one step.
+
+    The backward runs over the ``n_act`` tokens whose cotangents are not all
+    zero (zero-weight tokens contribute nothing), so its kernels are priced on
+    the work they do: n_act tokens."""
+    nb = N if n_act is None else n_act
     if name == "fwd_tile_kernel":
         return 2.0 * N * V * (K + D)             # S = h W^T, P E
     if name == "bwd_scores_kernel":
-        return 2.0 * N * V * (K + 2 * D)         # S recompute, dP = gO E^T, dE = P^T gO
+        return 2.0 * nb * V * (K + 2 * D)        # S recompute, dP = gO E^T, dE = P^T gO
     if name == "bwd_gemm_kernel":
-        return 4.0 * N * V * K                   # dh = dS W, dW = dS^T h
+        return 4.0 * nb * V * K                  # dh = dS W, dW = dS^T h
     return 0.0
 
 
@@ -204,15 +212,18 @@ def main():
 
     fwd_flops, flops = algorithmic_flops(N, K, V, D)
     tflops = flops / (ms * 1e-3) / 1e12
+    # tokens with a non-zero weight: the others have zero cotangents, and the
+    # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
+    n_act = int((weight != 0).sum().item()) if weight is not None else N
     per_kernel = {}
     for name, (kms, cnt) in kernels.items():
-        kf = kernel_flops(name, N, K, V, D) * args.steps
+        kf = kernel_flops(name, N, K, V, D, n_act) * args.steps
         per_kernel[name] = {"ms_per_step": round(kms / args.steps, 3), "launches_per_step": cnt // args.steps,
                             "avg_launch_ms": round(kms / cnt, 4),
                             "tflops": round(kf / (kms * 1e-3) / 1e12, 1) if kf else None}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     dk = per_kernel[dom]
-    launch_flops = kernel_flops(dom, N, K, V, D) * args.steps / (dk["launches_per_step"] * args.steps)
+    launch_flops = kernel_flops(dom, N, K, V, D, n_act) * args.steps / (dk["launches_per_step"] * args.steps)
     achieved = launch_flops / (dk["avg_launch_ms"] * 1e-3) / 1e12
     # W and E bytes the algorithm streams per step: fwd (W, E), bwd scores (W, E), dh GEMM (W)
     we_bytes = (3 * V * K + 2 * V * D) * 2
@@ -226,6 +237,8 @@ def main():
                                + (", bias" if cfg["bias"] else "") + (f", weight {cfg['weight']}" if cfg["weight"] else "")
                                + (f", z_loss {cfg['z']}" if cfg["z"] else ""),
                    "N": N, "K": K, "V": V, "D": D, "chunk": args.chunk},
+        "bwd_active_tokens": n_act,
+        "work_tflops": round((fwd_flops + (flops - fwd_flops) * n_act / N) / (ms * 1e-3) / 1e12, 1),
         "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
         "peak_gib": round(peak_gib, 3),

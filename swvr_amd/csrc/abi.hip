@@ -52,7 +52,7 @@ hipEvent_t take_event() {
 
 const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
-                                     "fill_zero_kernel",  "operand_packing"};
+                                     "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 

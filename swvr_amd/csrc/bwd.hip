@@ -29,37 +29,149 @@ __device__ __forceinline__ void store_as(void* base, int64_t idx, int dtype, flo
 }
 
 // ---------------------------------------------------------------- token-side packing
-// delta = rowsum(O * gO) - gLSE (swvr/chunked.py:113-114), and the token-side
-// operands of the scores kernel packed over N_pad rows: gO rounded to the
-// compute dtype (swvr/chunked.py:115) as [N_pad][DP] (zero padded), the same
-// values transposed per token block as [N_pad / BM][DP][BM] with the tokens
-// of a block in pe_row order (the A operand of dE^T = gO^T P), and
-// [lse | delta] as 2 x N_pad floats (lse = +inf on padding rows: P = 0 there).
+// The backward runs over the active tokens only: a token whose cotangents are
+// all zero (gO row = 0, gLSE = 0, so delta = 0) has dS = P (dP - delta) = 0
+// in every vocabulary row, so it adds nothing to gW, gE or gb and its gh row
+// is zero.  (A token with a non-finite O has a NaN delta and stays active, as
+// the reference propagates it.)  Zero-weight tokens of a weighted loss are
+// such tokens.  The active tokens are compacted in ascending order into
+// positions 0 .. n_act - 1; positions n_act .. N_pad - 1 are padding.
+
+// delta = rowsum(O * gO) - gLSE (swvr/chunked.py:113-114) and the active flag,
+// one thread per token.
+__global__ __launch_bounds__(256) void bwd_delta_kernel(const float* __restrict__ O, const float* __restrict__ gO,
+                                                        const float* __restrict__ glse, int N, int D,
+                                                        float* __restrict__ delta, int* __restrict__ flag) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float s = 0.f;
+  bool nz = false;
+  for (int k = 0; k < D; ++k) {
+    const float g = gO[(int64_t)n * D + k];
+    s += O[(int64_t)n * D + k] * g;
+    nz |= g != 0.f;
+  }
+  s -= glse[n];
+  delta[n] = s;
+  flag[n] = nz || glse[n] != 0.f || s != 0.f;  // NaN != 0
+}
+
+// Order-preserving compaction of the active tokens: idx[q] = token of
+// position q, inv[n] = position of token n or -1, n_act[0] = count.  One
+// workgroup; each thread scans IT consecutive tokens per round.
+__global__ __launch_bounds__(1024) void bwd_compact_kernel(const int* __restrict__ flag, int N, int* __restrict__ idx,
+                                                           int* __restrict__ inv, int* __restrict__ n_act) {
+  constexpr int IT = 16;
+  __shared__ int wsum[16];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int carry = 0;
+  for (int base = 0; base < N; base += 1024 * IT) {
+    const int n0 = base + t * IT;
+    int f[IT];
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      f[i] = n0 + i < N ? flag[n0 + i] : 0;
+      cnt += f[i];
+    }
+    int x = cnt;  // inclusive scan over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      before += j < w ? wsum[j] : 0;
+      total += wsum[j];
+    }
+    int q = carry + before + x - cnt;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int n = n0 + i;
+      if (n < N) {
+        inv[n] = f[i] ? q : -1;
+        if (f[i]) idx[q++] = n;
+      }
+    }
+    carry += total;
+    __syncthreads();  // wsum is rewritten next round
+  }
+  if (t == 0) n_act[0] = carry;
+}
+
+// The token-side operands of the scores kernel over positions: gO rounded to
+// the compute dtype (swvr/chunked.py:115) as [N_pad][DP] (zero padded), the
+// same values transposed per token block as [N_pad / BM][DP][BM] with the
+// positions of a block in pe_row order (the A operand of dE^T = gO^T P), and
+// [lse | delta] as 2 x N_pad floats (lse = +inf on padding: P = 0 there).
 template <class T>
-__global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__ O, const float* __restrict__ gO,
-                                                       const float* __restrict__ lse,
-                                                       const float* __restrict__ glse, int N, int D, int N_pad,
-                                                       int DP, int BM, T* __restrict__ gOp, T* __restrict__ gOt,
+__global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__ gO, const float* __restrict__ lse,
+                                                       const float* __restrict__ delta, const int* __restrict__ idx,
+                                                       const int* __restrict__ n_act, int D, int N_pad, int DP, int BM,
+                                                       T* __restrict__ gOp, T* __restrict__ gOt,
                                                        float* __restrict__ lsed) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= (int64_t)N_pad * DP) return;
-  const int n = (int)(e / DP), d = (int)(e % DP);
-  gOp[e] = (n < N && d < D) ? from_float<T>(gO[(int64_t)n * D + d]) : (T)0.f;
+  const int na = n_act[0];
+  const int q = (int)(e / DP), d = (int)(e % DP);
+  const int n = q < na ? idx[q] : -1;
+  gOp[e] = (n >= 0 && d < D) ? from_float<T>(gO[(int64_t)n * D + d]) : (T)0.f;
   {
     const int64_t blk = e / ((int64_t)DP * BM);
     const int rem = (int)(e - blk * DP * BM);
-    const int dt = rem / BM, q = rem % BM;
-    const int64_t nt = blk * BM + pe_row(q);
-    gOt[e] = (nt < N && dt < D) ? from_float<T>(gO[nt * D + dt]) : (T)0.f;
+    const int dt = rem / BM;
+    const int qt = (int)(blk * BM) + pe_row(rem % BM);
+    const int nt = qt < na ? idx[qt] : -1;
+    gOt[e] = (nt >= 0 && dt < D) ? from_float<T>(gO[(int64_t)nt * D + dt]) : (T)0.f;
   }
   if (d == 0) {
-    float s = 0.f;
-    if (n < N) {
-      for (int k = 0; k < D; ++k) s += O[(int64_t)n * D + k] * gO[(int64_t)n * D + k];
-      s -= glse[n];
-    }
-    lsed[n] = n < N ? lse[n] : kPosInf;
-    lsed[N_pad + n] = s;
+    lsed[q] = n >= 0 ? lse[n] : kPosInf;
+    lsed[N_pad + q] = n >= 0 ? delta[n] : 0.f;
+  }
+}
+
+// h rows of the active tokens in position order, [N_pad][K] (zeros past
+// n_act), 16 bytes per thread.
+template <class T>
+__global__ __launch_bounds__(256) void bwd_gather_rows_kernel(const T* __restrict__ h, int64_t ldh,
+                                                              const int* __restrict__ idx,
+                                                              const int* __restrict__ n_act, int N_pad, int K,
+                                                              T* __restrict__ hc) {
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int cpr = K / CE;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N_pad * cpr) return;
+  const int q = (int)(e / cpr), c = (int)(e % cpr);
+  const int n = q < n_act[0] ? idx[q] : -1;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (n >= 0) v = *reinterpret_cast<const uint4*>(h + (int64_t)n * ldh + (int64_t)c * CE);
+  *reinterpret_cast<uint4*>(hc + (int64_t)q * K + (int64_t)c * CE) = v;
+}
+
+// gh from the fp32 accumulator over positions: row n = dh_acc row inv[n], or
+// zero for an inactive token.  4 values per thread.
+__global__ __launch_bounds__(256) void bwd_expand_kernel(const float* __restrict__ dh_acc, const int* __restrict__ inv,
+                                                         int N, int K, void* __restrict__ gh, int gh_dtype) {
+  const int cpr = K / 4;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N * cpr) return;
+  const int n = (int)(e / cpr), c = (int)(e % cpr);
+  const int q = inv[n];
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (q >= 0) v = *reinterpret_cast<const float4*>(dh_acc + (int64_t)q * K + (int64_t)c * 4);
+  const int64_t o = (int64_t)n * K + (int64_t)c * 4;
+  if (gh_dtype == kBF16) {
+    bf16_t* g = static_cast<bf16_t*>(gh) + o;
+    g[0] = (bf16_t)v.x; g[1] = (bf16_t)v.y; g[2] = (bf16_t)v.z; g[3] = (bf16_t)v.w;
+  } else if (gh_dtype == kF16) {
+    f16_t* g = static_cast<f16_t*>(gh) + o;
+    g[0] = (f16_t)v.x; g[1] = (f16_t)v.y; g[2] = (f16_t)v.z; g[3] = (f16_t)v.w;
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(gh) + o) = v;
   }
 }
 
@@ -86,6 +198,7 @@ struct ScoresParams {
   float* part_dE;       // [G][DP][C]
   float* part_db;       // [G][C]
   int need_stage, need_dE, need_db;
+  const int* n_act;     // active positions (device)
 };
 
 // ---------------------------------------------------------------- dS stage layout
@@ -189,8 +302,10 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   const int vl0 = vt * BV;      // first chunk-local row of this tile
   const int vg0 = p.v0 + vl0;   // its global row
   const int rows = p.cv - vl0;  // valid rows of this tile (may exceed BV)
-  const int tb_begin = (int)((int64_t)g * p.n_tb / p.G);
-  const int tb_end = (int)((int64_t)(g + 1) * p.n_tb / p.G);
+  // token blocks of the active positions only, split evenly over the groups
+  const int n_tb_act = min(p.n_tb, (p.n_act[0] + BM - 1) / BM);
+  const int tb_begin = (int)((int64_t)g * n_tb_act / p.G);
+  const int tb_end = (int)((int64_t)(g + 1) * n_tb_act / p.G);
 
   // E and bias of the vocabulary tile: once per workgroup, ahead of the stages
   const uint32_t lds0 = lds_addr(smem);
@@ -407,8 +522,10 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   const int vl0 = vt * BV;      // first chunk-local row of this tile
   const int vg0 = p.v0 + vl0;   // its global row
   const int rows = p.cv - vl0;  // valid rows of this tile (may exceed BV)
-  const int tb_begin = (int)((int64_t)g * p.n_tb / p.G);
-  const int tb_end = (int)((int64_t)(g + 1) * p.n_tb / p.G);
+  // token blocks of the active positions only, split evenly over the groups
+  const int n_tb_act = min(p.n_tb, (p.n_act[0] + BM - 1) / BM);
+  const int tb_begin = (int)((int64_t)g * n_tb_act / p.G);
+  const int tb_end = (int)((int64_t)(g + 1) * n_tb_act / p.G);
   const int n_blocks = tb_end - tb_begin;
 
   f32x16_t deacc[DB][FV];
@@ -602,7 +719,7 @@ struct GemmParams {
   const void* stage;  // tiled dS (stage_off)
   int n_tb32;
   int64_t N_pad;
-  const void* h;
+  const void* h;   // h rows in position order
   int64_t ldh;
   const void* W;
   int64_t ldw;
@@ -612,11 +729,10 @@ struct GemmParams {
   int n_dw, n_dh;  // tile counts (0 when that gradient is not needed)
   void* gW;
   int gW_dtype;
-  float* dh_acc;
-  void* gh;
-  int gh_dtype;
-  int dh_first, dh_last;
+  float* dh_acc;   // dh over positions, fp32
+  int dh_first;
   float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
+  const int* n_act;  // active positions (device): the reduction length of dW, the rows of dh
 };
 
 // Store 4 fp32 values as OutT (one 16- or 8-byte buffer store at byte offset
@@ -873,8 +989,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
     ta.setup(p.stage, mt * GM, p.cv - mt * GM, p.n_tb32);
     PosRLoader<T, GN, kBK, NT> tb;
     tb.setup(static_cast<const T*>(p.h) + nt * GN, p.ldh, p.K - nt * GN, p.N);
-    // whole 32-position blocks: a partial block's tokens sit anywhere in it
-    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (p.N + 31) & ~31, wm * (GM / G::WM), wn * (GN / G::WN));
+    // whole 32-position blocks of the active positions (padding positions
+    // hold dS = 0 and zero rows of h)
+    gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (min(p.N, p.n_act[0]) + 31) & ~31, wm * (GM / G::WM),
+                              wn * (GN / G::WN));
   } else {
     StageBRLoader<T, GM, kBK, NT> ta;
     ta.setup(p.stage, mt * GM, p.n_tb32);
@@ -893,15 +1011,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
     else
       gemm_store<G>(acc, p.scale, static_cast<float*>(p.gW), nullptr, p.v0, rows, row0, col0, p.K, smem);
   } else {
+    // dh over positions accumulates in fp32; bwd_expand_kernel writes gh
     const float* prev = p.dh_first ? nullptr : p.dh_acc;
-    if (!p.dh_last)
-      gemm_store<G, FM, FN, true>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K, smem);
-    else if (p.gh_dtype == kBF16)
-      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<bf16_t*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
-    else if (p.gh_dtype == kF16)
-      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<f16_t*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
-    else
-      gemm_store<G, FM, FN, true>(acc, p.scale, static_cast<float*>(p.gh), prev, 0, rows, row0, col0, p.K, smem);
+    gemm_store<G, FM, FN, true>(acc, p.scale, p.dh_acc, prev, 0, rows, row0, col0, p.K, smem);
   }
 }
 
@@ -918,10 +1030,14 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   static_assert(kStages * SB <= G::LDS_BYTES, "ring fits");
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
   const int b = blockIdx.x;
-  if (b < p.n_dw)
+  if (b < p.n_dw) {
     gemm_tile<T, true>(p, xcd_swizzle(b, p.n_dw), smem);
-  else
-    gemm_tile<T, false>(p, xcd_swizzle(b - p.n_dw, p.n_dh), smem);
+  } else {
+    // dh tiles of the active positions' row blocks only (the grid covers all
+    // of N); the active tiles are spread over every XCD
+    const int n_dh = min(p.n_dh, (p.n_act[0] + G::GM - 1) / G::GM * p.n_n);
+    if (b - p.n_dw < n_dh) gemm_tile<T, false>(p, xcd_swizzle(b - p.n_dw, n_dh), smem);
+  }
 }
 
 // ---------------------------------------------------------------- dE / db
@@ -1028,11 +1144,20 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   float* biasp = reinterpret_cast<float*>(ws + plan.off_bias);
   T* hp = reinterpret_cast<T*>(ws + plan.off_hp);
   T* Wp = reinterpret_cast<T*>(ws + plan.off_Wp);
+  int* flag = reinterpret_cast<int*>(ws + plan.off_flag);
+  int* idx = reinterpret_cast<int*>(ws + plan.off_idx);
+  int* inv = reinterpret_cast<int*>(ws + plan.off_inv);
+  int* n_act = reinterpret_cast<int*>(ws + plan.off_nact);
+  float* delta = reinterpret_cast<float*>(ws + plan.off_delta);
+  T* hc = reinterpret_cast<T*>(ws + plan.off_hc);
 
   {
-    const int64_t n = (int64_t)plan.N_pad * plan.DP;
+    // delta, the active tokens, and the token-side operands over positions
     timing_begin(kKindBwdDelta, stream);
-    bwd_pack_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(p.O, p.gO, p.lse, p.glse, p.N, p.D,
+    bwd_delta_kernel<<<(p.N + 255) / 256, 256, 0, stream>>>(p.O, p.gO, p.glse, p.N, p.D, delta, flag);
+    bwd_compact_kernel<<<1, 1024, 0, stream>>>(flag, p.N, idx, inv, n_act);
+    const int64_t n = (int64_t)plan.N_pad * plan.DP;
+    bwd_pack_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(p.gO, p.lse, delta, idx, n_act, p.D,
                                                                    (int)plan.N_pad, plan.DP, plan.BM, gOp, gOt,
                                                                    lsed);
     timing_end(kKindBwdDelta, stream);
@@ -1042,8 +1167,13 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     pack_vocab_kernel<T><<<(int)((nv + 255) / 256), 256, 0, stream>>>(
         static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = launch_pack_rows<T>(static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, plan.N_pad, hp, stream)) !=
-        hipSuccess)
+    if (p.K > 0) {
+      const int64_t nh = plan.N_pad * (p.K / (16 / (int)sizeof(T)));
+      bwd_gather_rows_kernel<T><<<(int)((nh + 255) / 256), 256, 0, stream>>>(
+          static_cast<const T*>(p.h), p.ldh, idx, n_act, (int)plan.N_pad, p.K, hc);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
       return e;
     if ((e = launch_pack_rows<T>(static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream)) !=
         hipSuccess)
@@ -1083,6 +1213,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.need_stage = need_stage;
     sp.need_dE = p.gE != nullptr;
     sp.need_db = p.gb != nullptr;
+    sp.n_act = n_act;
     if ((e = dispatch_scores<T>(plan, sp, stream)) != hipSuccess) return e;
 
     if (need_stage) {
@@ -1090,8 +1221,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.stage = stage;
       gp.n_tb32 = (int)(plan.N_pad / 32);
       gp.N_pad = plan.N_pad;
-      gp.h = p.h;
-      gp.ldh = p.ldh;
+      gp.h = hc;
+      gp.ldh = p.K;
       gp.W = p.W;
       gp.ldw = p.ldw;
       gp.N = p.N;
@@ -1104,11 +1235,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.gW = p.gW;
       gp.gW_dtype = p.gW_dtype;
       gp.dh_acc = dh_acc;
-      gp.gh = p.gh;
-      gp.gh_dtype = p.gh_dtype;
       gp.dh_first = c == 0;
-      gp.dh_last = c == plan.n_chunks - 1;
       gp.scale = p.scale;
+      gp.n_act = n_act;
       if ((e = dispatch_gemm<T>(plan, gp, stream)) != hipSuccess) return e;
     }
     if (p.gE || p.gb) {
@@ -1118,6 +1247,15 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
                                                                             plan.DP, v0, cv, p.D, p.gE, p.gE_dtype,
                                                                             p.gb);
       timing_end(kKindBwdReduce, stream);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
+  if (p.gh) {
+    const int64_t ng = (int64_t)p.N * (p.K / 4);
+    if (ng > 0) {
+      timing_begin(kKindBwdExpand, stream);
+      bwd_expand_kernel<<<(int)((ng + 255) / 256), 256, 0, stream>>>(dh_acc, inv, p.N, p.K, p.gh, p.gh_dtype);
+      timing_end(kKindBwdExpand, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
   }
@@ -1193,7 +1331,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G < 1) G = 1;
   plan->G = G;
   plan->n_gpart = G * WT;  // dE / db partials: one per token group and token-wave row
-  plan->dh_acc = need_gh && plan->n_chunks > 1;
+  plan->dh_acc = need_gh;
   plan->V_pad = ((V + BV - 1) / BV) * BV;
   const size_t tb = dtype_bytes(dtype);
   size_t off = 0;
@@ -1221,6 +1359,18 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->N_pad * plan->hS * bk * tb);
   plan->off_Wp = off;
   off += align256((size_t)plan->V_pad * plan->hS * bk * tb);
+  plan->off_flag = off;
+  off += align256((size_t)plan->N_pad * 4);
+  plan->off_idx = off;
+  off += align256((size_t)plan->N_pad * 4);
+  plan->off_inv = off;
+  off += align256((size_t)plan->N_pad * 4);
+  plan->off_nact = off;
+  off += 256;
+  plan->off_delta = off;
+  off += align256((size_t)plan->N_pad * 4);
+  plan->off_hc = off;
+  off += align256((size_t)plan->N_pad * K * tb);
   plan->ws_bytes = off;
   return true;
 }

@@ -16,6 +16,7 @@ enum KernelKind {
   kKindBwdReduce,
   kKindFill,
   kKindPack,
+  kKindBwdExpand,
   kNumKinds
 };
 
@@ -71,10 +72,11 @@ struct BwdPlan {
   int n_chunks;
   int G;                 // token groups of the dS kernel
   int n_gpart;           // dE / db partials per chunk
-  bool dh_acc;           // dh needs an fp32 accumulator across chunks
+  bool dh_acc;           // dh accumulates in fp32 (over the active tokens), then expands into gh
   int V_pad;             // vocabulary rows of the packed E / bias
   int hS;                // reduction slices of the packed h and W
-  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, off_Wp, ws_bytes;
+  size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, off_Wp;
+  size_t off_flag, off_idx, off_inv, off_nact, off_delta, off_hc, ws_bytes;
 };
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,

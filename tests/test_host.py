@@ -46,9 +46,9 @@ def test_workspace_sizes():
     fwd = lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, D)
     assert 0 < fwd < 2**30
     bwd = lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 8192, 1)
-    # dS stage (N x 8192 bf16) + fp32 dh accumulator + packed h and W (bf16) + small partials:
-    # O(N * chunk + (N + V) * K)
-    need = N * 8192 * 2 + N * K * 4 + (N + V) * K * 2
+    # dS stage (N x 8192 bf16) + fp32 dh accumulator + packed h and W and the position-ordered
+    # h (bf16) + small partials: O(N * chunk + (N + V) * K)
+    need = N * 8192 * 2 + N * K * 4 + (2 * N + V) * K * 2
     assert need <= bwd < need + 2**27
     assert lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 0, 1) == 0
     assert lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 256) == 0   # fp32 caps D at 128
