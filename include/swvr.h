@@ -78,6 +78,33 @@ int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
              float* O, float* lse, void* workspace, size_t workspace_bytes,
              void* stream);
 
+/* Vocabulary-parallel forward, one shard.  With W, E and bias holding V rows of
+ * the vocabulary (a shard), writes the shard's softmax partials, fp32:
+ *   m[n]     = max_v S[n,v]
+ *   l[n]     = sum_v exp(S[n,v] - m[n])
+ *   acc[n,:] = sum_v exp(S[n,v] - m[n]) E[v,:]      (row stride D, unnormalised)
+ * with m = -inf, l = 0, acc = 0 for a row whose shard scores are all -inf.
+ * Each rank of a vocabulary-parallel job runs it on its shard, the partials are
+ * all-gathered (N (D + 2) floats per shard) and swvr_combine merges them; the
+ * backward then runs swvr_bwd on each shard with the merged O and lse and sums
+ * gh over the shards.  Workspace: swvr_fwd_workspace_size of the shard.
+ * No reference counterpart: it is the shard-local half of the reference's
+ * online softmax (swvr/chunked.py:82-105). */
+int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                     const void* h, int64_t ldh, const void* W, int64_t ldw,
+                     const void* E, int64_t lde, const float* bias, float logit_scale,
+                     float* m, float* l, float* acc, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Merge S shards' partials in shard order (deterministic): m, l are [S][N],
+ * acc is [S][N][D] (each shard's swvr_fwd_partial output, stacked), into
+ * O [N,D] and lse [N], as swvr_fwd would give for the whole vocabulary:
+ * O = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), lse = M + log(sum),
+ * M = max_s m_s (the -inf guard of swvr/chunked.py:98-99 included).
+ * No reference counterpart (the vocabulary-parallel combine). */
+int swvr_combine(int64_t S, int64_t N, int64_t D, const float* m, const float* l,
+                 const float* acc, float* O, float* lse, void* stream);
+
 /* Workspace bytes swvr_bwd needs.  `chunk` is the vocabulary staging chunk
  * (the reference's chunk_size, swvr/chunked.py:120): the backward stages
  * dS for `chunk` vocabulary rows at a time, so this is O(N * chunk). */

@@ -99,6 +99,42 @@ void timing_end(int kind, hipStream_t stream) {
   if (e && hipEventRecord(e, stream) == hipSuccess) g_launches.push_back({kind, s, e});
 }
 
+namespace {
+
+int fwd_common(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
+               int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, float* O, float* lse,
+               float* m_out, float* l_out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
+  if (rc != SWVR_OK) return rc;
+  if (N > 0 && ((D > 0 && !O) || (m_out ? !l_out : !lse)))
+    return fail(SWVR_EINVAL, m_out ? "m, l and acc must be non-null" : "O and lse must be non-null");
+  FwdPlan plan;
+  if (!fwd_plan(dtype, N, K, V, D, &plan)) return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (N == 0) return SWVR_OK;
+  if (!workspace || workspace_bytes < plan.ws_bytes)
+    return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+  FwdParams p;
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  hipError_t e = fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, m_out, l_out,
+                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return SWVR_OK;
+}
+
+}  // namespace
+
 }  // namespace swvr
 
 using namespace swvr;
@@ -124,30 +160,31 @@ size_t swvr_fwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64
 int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
              int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, float* O, float* lse,
              void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr, nullptr, workspace,
+                    workspace_bytes, stream);
+}
+
+int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh,
+                     const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale,
+                     float* m, float* l, float* acc, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!m && N > 0) {
+    g_err[0] = 0;
+    return fail(SWVR_EINVAL, "m, l and acc must be non-null");
+  }
+  return fwd_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, acc, nullptr, m, l, workspace,
+                    workspace_bytes, stream);
+}
+
+int swvr_combine(int64_t S, int64_t N, int64_t D, const float* m, const float* l, const float* acc, float* O,
+                 float* lse, void* stream) {
   g_err[0] = 0;
-  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
-  if (rc != SWVR_OK) return rc;
-  if (N > 0 && ((D > 0 && !O) || !lse)) return fail(SWVR_EINVAL, "O and lse must be non-null");
-  FwdPlan plan;
-  if (!fwd_plan(dtype, N, K, V, D, &plan)) return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (S < 1 || N < 0 || D < 0) return fail(SWVR_EINVAL, "bad sizes S=%lld N=%lld D=%lld", (long long)S, (long long)N,
+                                           (long long)D);
+  if (S > INT32_MAX || N > INT32_MAX || D > INT32_MAX) return fail(SWVR_EINVAL, "sizes must fit in 32 bits");
   if (N == 0) return SWVR_OK;
-  if (!workspace || workspace_bytes < plan.ws_bytes)
-    return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
-  FwdParams p;
-  p.h = h;
-  p.ldh = ldh;
-  p.W = W;
-  p.ldw = ldw;
-  p.E = E;
-  p.lde = lde;
-  p.bias = bias;
-  p.scale = logit_scale;
-  p.N = (int)N;
-  p.K = (int)K;
-  p.V = (int)V;
-  p.D = (int)D;
-  hipError_t e = fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, "forward launch");
+  if (!m || !l || !lse || (D > 0 && (!acc || !O))) return fail(SWVR_EINVAL, "m, l, acc, O and lse must be non-null");
+  hipError_t e = shard_combine((int)S, (int)N, (int)D, m, l, acc, O, lse, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
   return SWVR_OK;
 }
 

@@ -253,16 +253,21 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   }
 }
 
-// Merge the partial softmaxes in a fixed order: O = sum_p acc_p e^(m_p - M) /
+// Merge partial softmaxes in a fixed order: O = sum_p acc_p e^(m_p - M) /
 // sum_p l_p e^(m_p - M), LSE = M + log(...).  A row with every score -inf ends
 // with M = -inf, L = 0: O = NaN and LSE = -inf, as swvr/chunked.py:105 gives.
-// One thread per (d, n) with n fastest (coalesced partial reads); the d = 0
-// thread of a row also writes its LSE.
+// Partial p of (row n, column d) of acc sits at p * sp + d * sd + n * sn, so
+// one kernel merges the forward's own partials ([n_part][DP][N], token
+// fastest) and vocabulary shards' ([S][N][D]).  With m_out set, it writes the
+// merged partial (M, L and the unnormalised acc, [N][D]) instead of O / LSE.
+// One thread per (d, n) with n fastest; the d = 0 thread of a row also writes
+// its LSE (or M, L).
 __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restrict__ part_m,
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_acc, int n_part, int N,
-                                                          int D, int DP, float* __restrict__ O,
-                                                          float* __restrict__ lse) {
+                                                          int D, int64_t sp, int64_t sd, int64_t sn,
+                                                          float* __restrict__ O, float* __restrict__ lse,
+                                                          float* __restrict__ m_out, float* __restrict__ l_out) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int Dw = D > 0 ? D : 1;
   if (e >= (int64_t)N * Dw) return;
@@ -274,10 +279,18 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   for (int q = 0; q < n_part; ++q) {
     const float wq = expf(part_m[(int64_t)q * N + n] - shift);
     L += part_l[(int64_t)q * N + n] * wq;
-    if (d < D) a += part_acc[((int64_t)q * DP + d) * N + n] * wq;
+    if (d < D) a += part_acc[q * sp + d * sd + n * sn] * wq;
   }
-  if (d < D) O[(int64_t)n * D + d] = a / L;
-  if (d == 0) lse[n] = M + logf(L);
+  if (m_out) {
+    if (d < D) O[(int64_t)n * D + d] = a;
+    if (d == 0) {
+      m_out[n] = M;
+      l_out[n] = L;
+    }
+  } else {
+    if (d < D) O[(int64_t)n * D + d] = a / L;
+    if (d == 0) lse[n] = M + logf(L);
+  }
 }
 
 template <class T, int DP>
@@ -398,8 +411,8 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   return true;
 }
 
-hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse,
-                      hipStream_t stream) {
+hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse, float* m_out,
+                      float* l_out, hipStream_t stream) {
   if (p.N == 0) return hipSuccess;
   p.n_tb = plan.n_tb;
   p.n_split = plan.n_split;
@@ -422,8 +435,19 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
   if (e != hipSuccess) return e;
   timing_begin(kKindFwdCombine, stream);
   const int64_t n_threads = (int64_t)p.N * (p.D > 0 ? p.D : 1);
-  fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(p.part_m, p.part_l, p.part_acc, plan.n_part,
-                                                                         p.N, p.D, plan.DP, O, lse);
+  fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
+      p.part_m, p.part_l, p.part_acc, plan.n_part, p.N, p.D, (int64_t)plan.DP * p.N, p.N, 1, O, lse, m_out, l_out);
+  timing_end(kKindFwdCombine, stream);
+  return hipGetLastError();
+}
+
+hipError_t shard_combine(int S, int N, int D, const float* m, const float* l, const float* acc, float* O, float* lse,
+                         hipStream_t stream) {
+  const int64_t n_threads = (int64_t)N * (D > 0 ? D : 1);
+  if (n_threads == 0) return hipSuccess;
+  timing_begin(kKindFwdCombine, stream);
+  fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(m, l, acc, S, N, D, (int64_t)N * D, 1, D, O,
+                                                                         lse, nullptr, nullptr);
   timing_end(kKindFwdCombine, stream);
   return hipGetLastError();
 }

@@ -58,8 +58,13 @@ struct FwdPlan {
 // Tile shape, split count and workspace for a forward call; ok=false if the
 // dtype / D combination is unsupported.
 bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan);
-hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse,
-                      hipStream_t stream);
+// O / lse, or with m_out / l_out set the merged partial softmax (m, l, and the
+// unnormalised acc in O) of the vocabulary rows given.
+hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse, float* m_out,
+                      float* l_out, hipStream_t stream);
+// Merge S vocabulary shards' partials (m, l: [S][N]; acc: [S][N][D]) in shard order.
+hipError_t shard_combine(int S, int N, int D, const float* m, const float* l, const float* acc, float* O, float* lse,
+                         hipStream_t stream);
 
 // ---------------------------------------------------------------- backward
 struct BwdPlan {

@@ -77,6 +77,17 @@ def test_abi_rejects_bad_arguments_without_touching_the_device(kw, code):
     assert _lib.load().swvr_last_error()
 
 
+def test_abi_combine_rejects_bad_arguments_without_touching_the_device():
+    lib = _lib.load()
+    assert lib.swvr_combine(0, 4, 4, None, None, None, None, None, None) == _lib.EINVAL
+    assert b"S=0" in lib.swvr_last_error()
+    assert lib.swvr_combine(2, 4, 4, None, None, None, None, None, None) == _lib.EINVAL
+    assert lib.swvr_combine(2, 0, 4, None, None, None, None, None, None) == _lib.OK  # no rows: nothing to do
+    p = ctypes.c_void_p(16)
+    assert lib.swvr_fwd_partial(_lib.BF16, 4, 16, 8, 4, p, 16, p, 16, p, 4, None, 1.0,
+                                None, None, None, p, 1 << 20, None) == _lib.EINVAL
+
+
 def test_abi_bwd_rejects_bad_chunk_and_gradient_dtype():
     lib = _lib.load()
     p = ctypes.c_void_p(16)
