@@ -78,6 +78,17 @@ int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
              float* O, float* lse, void* workspace, size_t workspace_bytes,
              void* stream);
 
+/* swvr_fwd with h and W stored in their own dtypes: h_dtype / w_dtype is the
+ * compute dtype, or SWVR_F32 under a 2-byte compute dtype.  fp32 rows are
+ * rounded to the compute dtype as they are packed, so autocast with fp32
+ * weights needs no separate cast of W or h (the reference casts
+ * W[v0:v1].to(cdt) per chunk, swvr/chunked.py:92,123,146).  The alignment
+ * contract is the same, in elements.  Workspace: swvr_fwd_workspace_size. */
+int swvr_fwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                   const void* h, int64_t ldh, const void* W, int64_t ldw,
+                   const void* E, int64_t lde, const float* bias, float logit_scale,
+                   float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Vocabulary-parallel forward, one shard.  With W, E and bias holding V rows of
  * the vocabulary (a shard), writes the shard's softmax partials, fp32:
  *   m[n]     = max_v S[n,v]
@@ -125,6 +136,19 @@ int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
              int64_t chunk,
              void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
              float* gb, void* workspace, size_t workspace_bytes, void* stream);
+
+/* swvr_bwd with h and W stored in their own dtypes, as swvr_fwd_mixed.  With
+ * an fp32 W the workspace also holds a copy of W in the compute dtype (the dh
+ * product reads W rows): size it with swvr_bwd_workspace_size_mixed. */
+size_t swvr_bwd_workspace_size_mixed(int dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                                     int64_t chunk, int need_gh);
+int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                   const void* h, int64_t ldh, const void* W, int64_t ldw,
+                   const void* E, int64_t lde, const float* bias, float logit_scale,
+                   const float* O, const float* lse, const float* gO, const float* glse,
+                   int64_t chunk,
+                   void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
+                   float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Instrumentation (no reference counterpart).  While enabled, every kernel
  * launch is bracketed by a pair of HIP events on its stream.

@@ -49,6 +49,16 @@ def _matrix(x, cdt, Kp):
     return x
 
 
+def _operand(x, cdt, Kp):
+    """``(tensor, dtype tag)`` of h or W for the C ABI: an fp32 matrix under a 2-byte compute
+    dtype (autocast with fp32 weights) goes as it is, and the kernels round it while packing;
+    anything else goes through ``_matrix``."""
+    if (x.dtype == torch.float32 and cdt in (torch.bfloat16, torch.float16) and x.shape[1] == Kp
+            and x.stride(1) == 1 and (x.shape[0] <= 1 or x.stride(0) % 8 == 0) and x.data_ptr() % 16 == 0):
+        return x, _lib.F32
+    return _matrix(x, cdt, Kp), _lib.DTYPE_TAG[cdt]
+
+
 def _embed(E, cdt):
     if E.dtype != cdt:
         E = E.to(cdt)
@@ -67,7 +77,7 @@ def _forward(h, W, E, bias, logit_scale, chunk, cdt):
     N, K = h.shape
     V, D = E.shape
     Kp = _kpad(K)
-    hc, Wc, Ec = _matrix(h, cdt, Kp), _matrix(W, cdt, Kp), _embed(E, cdt)
+    (hc, h_tag), (Wc, w_tag), Ec = _operand(h, cdt, Kp), _operand(W, cdt, Kp), _embed(E, cdt)
     b = bias.to(torch.float32).contiguous() if bias is not None else None
     O = torch.empty(N, D, dtype=torch.float32, device=h.device)
     lse = torch.empty(N, dtype=torch.float32, device=h.device)
@@ -75,9 +85,9 @@ def _forward(h, W, E, bias, logit_scale, chunk, cdt):
     ws_bytes = lib.swvr_fwd_workspace_size(tag, N, Kp, V, D)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
     with torch.cuda.device(h.device):
-        rc = lib.swvr_fwd(tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc), _lead_stride(Wc),
-                          _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
-                          _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_of(h.device))
+        rc = lib.swvr_fwd_mixed(tag, h_tag, w_tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc),
+                                _lead_stride(Wc), _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
+                                _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_of(h.device))
     _lib.check(rc)
     return O, lse
 
@@ -95,7 +105,7 @@ def _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, 
     N, K = h.shape
     V, D = E.shape
     Kp = _kpad(K)
-    hc, Wc, Ec = _matrix(h, cdt, Kp), _matrix(W, cdt, Kp), _embed(E, cdt)
+    (hc, h_tag), (Wc, w_tag), Ec = _operand(h, cdt, Kp), _operand(W, cdt, Kp), _embed(E, cdt)
     b = bias.to(torch.float32).contiguous() if bias is not None else None
     dev = h.device
     gh = _grad_buffer((N, Kp), h.dtype, dev) if need_h else None
@@ -107,18 +117,18 @@ def _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, 
     O32 = O.to(torch.float32).contiguous()
     lse32 = lse.to(torch.float32).contiguous()
     tag = _lib.DTYPE_TAG[cdt]
-    ws_bytes = lib.swvr_bwd_workspace_size(tag, N, Kp, V, D, int(chunk), int(need_h))
+    ws_bytes = lib.swvr_bwd_workspace_size_mixed(tag, w_tag, N, Kp, V, D, int(chunk), int(need_h))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     def tag_of(t):
         return _lib.DTYPE_TAG[t.dtype] if t is not None else 0
 
     with torch.cuda.device(dev):
-        rc = lib.swvr_bwd(tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc), _lead_stride(Wc),
-                          _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
-                          _lib.ptr(O32), _lib.ptr(lse32), _lib.ptr(gO32), _lib.ptr(glse32), int(chunk),
-                          _lib.ptr(gh), tag_of(gh), _lib.ptr(gW), tag_of(gW), _lib.ptr(gE), tag_of(gE),
-                          _lib.ptr(gb), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
+        rc = lib.swvr_bwd_mixed(tag, h_tag, w_tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc),
+                                _lead_stride(Wc), _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
+                                _lib.ptr(O32), _lib.ptr(lse32), _lib.ptr(gO32), _lib.ptr(glse32), int(chunk),
+                                _lib.ptr(gh), tag_of(gh), _lib.ptr(gW), tag_of(gW), _lib.ptr(gE), tag_of(gE),
+                                _lib.ptr(gb), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
     _lib.check(rc)
     if gh is not None:
         gh = gh[:, :K] if Kp != K else gh

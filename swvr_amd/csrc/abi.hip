@@ -101,12 +101,24 @@ void timing_end(int kind, hipStream_t stream) {
 
 namespace {
 
-int fwd_common(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
-               int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, float* O, float* lse,
-               float* m_out, float* l_out, void* workspace, size_t workspace_bytes, void* stream) {
+// Storage dtype of h or W: the compute dtype, or fp32 under a 2-byte compute dtype.
+int check_storage(int dtype, int h_dtype, int w_dtype) {
+  const bool two = dtype == SWVR_BF16 || dtype == SWVR_F16;
+  if (!(h_dtype == dtype || (two && h_dtype == SWVR_F32)))
+    return fail(SWVR_EDTYPE, "h dtype tag %d with compute dtype %d", h_dtype, dtype);
+  if (!(w_dtype == dtype || (two && w_dtype == SWVR_F32)))
+    return fail(SWVR_EDTYPE, "W dtype tag %d with compute dtype %d", w_dtype, dtype);
+  return SWVR_OK;
+}
+
+int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
+               int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
+               float logit_scale, float* O, float* lse, float* m_out, float* l_out, void* workspace,
+               size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
   if (rc != SWVR_OK) return rc;
+  if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
   if (N > 0 && ((D > 0 && !O) || (m_out ? !l_out : !lse)))
     return fail(SWVR_EINVAL, m_out ? "m, l and acc must be non-null" : "O and lse must be non-null");
   FwdPlan plan;
@@ -127,6 +139,8 @@ int fwd_common(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void
   p.K = (int)K;
   p.V = (int)V;
   p.D = (int)D;
+  p.h_f32 = h_dtype != dtype;
+  p.w_f32 = w_dtype != dtype;
   hipError_t e = fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, m_out, l_out,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "forward launch");
@@ -160,8 +174,15 @@ size_t swvr_fwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64
 int swvr_fwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
              int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, float* O, float* lse,
              void* workspace, size_t workspace_bytes, void* stream) {
-  return fwd_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr, nullptr, workspace,
-                    workspace_bytes, stream);
+  return fwd_common(dtype, dtype, dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr,
+                    nullptr, workspace, workspace_bytes, stream);
+}
+
+int swvr_fwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
+                   int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
+                   float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_common(dtype, h_dtype, w_dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr,
+                    nullptr, workspace, workspace_bytes, stream);
 }
 
 int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh,
@@ -171,8 +192,8 @@ int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, cons
     g_err[0] = 0;
     return fail(SWVR_EINVAL, "m, l and acc must be non-null");
   }
-  return fwd_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, acc, nullptr, m, l, workspace,
-                    workspace_bytes, stream);
+  return fwd_common(dtype, dtype, dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, acc, nullptr, m, l,
+                    workspace, workspace_bytes, stream);
 }
 
 int swvr_combine(int64_t S, int64_t N, int64_t D, const float* m, const float* l, const float* acc, float* O,
@@ -188,20 +209,28 @@ int swvr_combine(int64_t S, int64_t N, int64_t D, const float* m, const float* l
   return SWVR_OK;
 }
 
-size_t swvr_bwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, int need_gh) {
+size_t swvr_bwd_workspace_size_mixed(int dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                                     int64_t chunk, int need_gh) {
   BwdPlan plan;
-  if (N < 0 || V < 0 || D < 0 || chunk <= 0 || !bwd_plan(dtype, N, K, V, D, chunk, need_gh != 0, &plan)) return 0;
+  if (N < 0 || V < 0 || D < 0 || chunk <= 0 ||
+      !bwd_plan(dtype, N, K, V, D, chunk, need_gh != 0, &plan, w_dtype != dtype))
+    return 0;
   return plan.ws_bytes;
 }
 
-int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
-             int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, const float* O,
-             const float* lse, const float* gO, const float* glse, int64_t chunk, void* gh, int gh_dtype, void* gW,
-             int gW_dtype, void* gE, int gE_dtype, float* gb, void* workspace, size_t workspace_bytes,
-             void* stream) {
+size_t swvr_bwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, int need_gh) {
+  return swvr_bwd_workspace_size_mixed(dtype, dtype, N, K, V, D, chunk, need_gh);
+}
+
+int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
+                   int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
+                   float logit_scale, const float* O, const float* lse, const float* gO, const float* glse,
+                   int64_t chunk, void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype, float* gb,
+                   void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = 0;
   int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
   if (rc != SWVR_OK) return rc;
+  if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
   if (chunk <= 0) return fail(SWVR_EINVAL, "chunk must be positive, got %lld", (long long)chunk);
   if (gh && !is_dtype(gh_dtype)) return fail(SWVR_EDTYPE, "unsupported gh dtype tag %d", gh_dtype);
   if (gW && !is_dtype(gW_dtype)) return fail(SWVR_EDTYPE, "unsupported gW dtype tag %d", gW_dtype);
@@ -209,7 +238,7 @@ int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* 
   if (gb && !bias) return fail(SWVR_EINVAL, "gb requested without a bias");
   if (N > 0 && (!lse || !glse || (D > 0 && (!O || !gO)))) return fail(SWVR_EINVAL, "O, lse, gO and glse must be non-null");
   BwdPlan plan;
-  if (!bwd_plan(dtype, N, K, V, D, chunk, gh != nullptr, &plan))
+  if (!bwd_plan(dtype, N, K, V, D, chunk, gh != nullptr, &plan, w_dtype != dtype))
     return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
   if (N > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
     return fail(SWVR_EWORKSPACE, "backward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
@@ -238,9 +267,20 @@ int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* 
   p.gE_dtype = gE_dtype;
   p.gb = gb;
   p.ws = static_cast<char*>(workspace);
+  p.h_f32 = h_dtype != dtype;
+  p.w_f32 = w_dtype != dtype;
   hipError_t e = bwd_launch(dtype, plan, p, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "backward launch");
   return SWVR_OK;
+}
+
+int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,
+             int64_t ldw, const void* E, int64_t lde, const float* bias, float logit_scale, const float* O,
+             const float* lse, const float* gO, const float* glse, int64_t chunk, void* gh, int gh_dtype, void* gW,
+             int gW_dtype, void* gE, int gE_dtype, float* gb, void* workspace, size_t workspace_bytes,
+             void* stream) {
+  return swvr_bwd_mixed(dtype, dtype, dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, gO, glse,
+                        chunk, gh, gh_dtype, gW, gW_dtype, gE, gE_dtype, gb, workspace, workspace_bytes, stream);
 }
 
 int swvr_timing_enable(int on) {

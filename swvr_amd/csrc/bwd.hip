@@ -135,9 +135,9 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(const float* __restrict__
 }
 
 // h rows of the active tokens in position order, [N_pad][K] (zeros past
-// n_act), 16 bytes per thread.
-template <class T>
-__global__ __launch_bounds__(256) void bwd_gather_rows_kernel(const T* __restrict__ h, int64_t ldh,
+// n_act), 16 bytes of T per thread; h may be fp32 for a 2-byte T (rounded here).
+template <class Src, class T>
+__global__ __launch_bounds__(256) void bwd_gather_rows_kernel(const Src* __restrict__ h, int64_t ldh,
                                                               const int* __restrict__ idx,
                                                               const int* __restrict__ n_act, int N_pad, int K,
                                                               T* __restrict__ hc) {
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void bwd_gather_rows_kernel(const T* __restric
   const int q = (int)(e / cpr), c = (int)(e % cpr);
   const int n = q < n_act[0] ? idx[q] : -1;
   uint4 v = make_uint4(0, 0, 0, 0);
-  if (n >= 0) v = *reinterpret_cast<const uint4*>(h + (int64_t)n * ldh + (int64_t)c * CE);
+  if (n >= 0) v = load_chunk<Src, T>(h + (int64_t)n * ldh + (int64_t)c * CE);
   *reinterpret_cast<uint4*>(hc + (int64_t)q * K + (int64_t)c * CE) = v;
 }
 
@@ -180,8 +180,6 @@ struct ScoresParams {
   const void* hp;       // h packed in its tiles' LDS image (pack_rows_tiled_kernel)
   const void* Wp;       // W packed the same way, [V_pad] rows
   int hS;               // reduction slices of both
-  const void* W;
-  int64_t ldw;
   const void* Ep;       // packed E [V_pad][DP]
   const float* biasp;   // packed bias [V_pad]
   float scale;
@@ -1150,6 +1148,10 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   int* n_act = reinterpret_cast<int*>(ws + plan.off_nact);
   float* delta = reinterpret_cast<float*>(ws + plan.off_delta);
   T* hc = reinterpret_cast<T*>(ws + plan.off_hc);
+  // W in the compute dtype, row-major: the caller's, or a copy made while packing an fp32 W
+  T* Wc = (sizeof(T) == 2 && p.w_f32) ? reinterpret_cast<T*>(ws + plan.off_Wc) : nullptr;
+  const void* Wr = Wc ? static_cast<const void*>(Wc) : p.W;
+  const int64_t ldwr = Wc ? p.K : p.ldw;
 
   {
     // delta, the active tokens, and the token-side operands over positions
@@ -1169,14 +1171,19 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (p.K > 0) {
       const int64_t nh = plan.N_pad * (p.K / (16 / (int)sizeof(T)));
-      bwd_gather_rows_kernel<T><<<(int)((nh + 255) / 256), 256, 0, stream>>>(
-          static_cast<const T*>(p.h), p.ldh, idx, n_act, (int)plan.N_pad, p.K, hc);
+      const unsigned gb = (unsigned)((nh + 255) / 256);
+      if (sizeof(T) == 2 && p.h_f32)
+        bwd_gather_rows_kernel<float, T><<<gb, 256, 0, stream>>>(static_cast<const float*>(p.h), p.ldh, idx,
+                                                                  n_act, (int)plan.N_pad, p.K, hc);
+      else
+        bwd_gather_rows_kernel<T, T><<<gb, 256, 0, stream>>>(static_cast<const T*>(p.h), p.ldh, idx, n_act,
+                                                              (int)plan.N_pad, p.K, hc);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
       return e;
-    if ((e = launch_pack_rows<T>(static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream)) !=
-        hipSuccess)
+    // fp32 W: the packing also writes the row-major copy the dh product reads
+    if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream, Wc)) != hipSuccess)
       return e;
     timing_end(kKindPack, stream);
   }
@@ -1189,8 +1196,6 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.hp = hp;
     sp.Wp = Wp;
     sp.hS = plan.hS;
-    sp.W = p.W;
-    sp.ldw = p.ldw;
     sp.Ep = Ep;
     sp.biasp = biasp;
     sp.scale = p.scale;
@@ -1223,8 +1228,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.N_pad = plan.N_pad;
       gp.h = hc;
       gp.ldh = p.K;
-      gp.W = p.W;
-      gp.ldw = p.ldw;
+      gp.W = Wr;
+      gp.ldw = ldwr;
       gp.N = p.N;
       gp.K = p.K;
       gp.v0 = v0;
@@ -1296,7 +1301,8 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 
 }  // namespace
 
-bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan) {
+bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan,
+              bool w_f32) {
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
   int BM, BV, GM, GN, WT, wgs;
@@ -1371,6 +1377,8 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->N_pad * 4);
   plan->off_hc = off;
   off += align256((size_t)plan->N_pad * K * tb);
+  plan->off_Wc = off;
+  if (w_f32 && tb == 2) off += align256((size_t)V * K * tb);
   plan->ws_bytes = off;
   return true;
 }

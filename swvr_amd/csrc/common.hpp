@@ -758,6 +758,24 @@ struct CountedRing {
 };
 
 // ----------------------------------------------------------------------------
+// One 16-byte chunk of CE = 16 / sizeof(T) elements in T, read from a source
+// of type Src: one 16-byte load when Src is T; two for fp32 rounded to a
+// 2-byte T (the cast of autocast with fp32 weights, fused into the packing).
+template <class Src, class T>
+__device__ __forceinline__ uint4 load_chunk(const Src* p) {
+  if constexpr (sizeof(Src) == sizeof(T)) {
+    return *reinterpret_cast<const uint4*>(p);
+  } else {
+    static_assert(sizeof(Src) == 4 && sizeof(T) == 2, "fp32 source, 2-byte dtype");
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    T q[8] = {from_float<T>(a.x), from_float<T>(a.y), from_float<T>(a.z), from_float<T>(a.w),
+              from_float<T>(b.x), from_float<T>(b.y), from_float<T>(b.z), from_float<T>(b.w)};
+    uint4 u;
+    __builtin_memcpy(&u, q, 16);
+    return u;
+  }
+}
+
 // Token rows (h) packed in the LDS image of their operand tiles:
 // [N_pad / 32][S = K_pad / BK][32 rows][BK], each 16-byte chunk already at its
 // XOR-swizzled place (KTile layout), zeros past N and K.  A tile of any
@@ -765,9 +783,11 @@ struct CountedRing {
 // (full cache lines instead of one 64-byte piece per row) with no bounds.
 // One workgroup per 32 rows x 8 slices: the rows are read as contiguous
 // 512-byte runs into LDS, the 8 slices written as one contiguous 16 KB run.
-template <class T>
-__global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const T* __restrict__ src, int64_t ld, int N, int K,
-                                                              int S, T* __restrict__ dst) {
+// The source may be fp32 for a 2-byte T (rounded here); with rowmajor set,
+// the rows are also written as a plain [N][K] copy in T.
+template <class Src, class T>
+__global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restrict__ src, int64_t ld, int N, int K,
+                                                              int S, T* __restrict__ dst, T* __restrict__ rowmajor) {
   constexpr int BK = SliceK<T>::value, CE = 16 / (int)sizeof(T), CPR = BK / CE;
   static_assert(CPR == 4, "4 chunks per slice row");
   constexpr int SPW = 8;                    // slices per workgroup
@@ -783,7 +803,10 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const T* __restric
     const int64_t n = (int64_t)grp * 32 + row;
     const int k = (s0 * CPR + kc) * CE;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (kc < ns * CPR && n < N && k < K) v = *reinterpret_cast<const uint4*>(src + n * ld + k);
+    if (kc < ns * CPR && n < N && k < K) {
+      v = load_chunk<Src, T>(src + n * ld + k);
+      if (rowmajor) *reinterpret_cast<uint4*>(rowmajor + n * K + k) = v;
+    }
     tile[row * RSTRIDE + kc] = v;
   }
   __syncthreads();
@@ -798,13 +821,25 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const T* __restric
 }
 
 // Pack rows [rows_pad][K] of src (rows_pad a multiple of 32) into the tile image.
-template <class T>
-__host__ hipError_t launch_pack_rows(const T* src, int64_t ld, int N, int K, int S, int64_t rows_pad, T* dst,
-                                     hipStream_t stream) {
+template <class T, class Src = T>
+__host__ hipError_t launch_pack_rows(const Src* src, int64_t ld, int N, int K, int S, int64_t rows_pad, T* dst,
+                                     hipStream_t stream, T* rowmajor = nullptr) {
   const int64_t blocks = (rows_pad / 32) * ((S + 7) / 8);
   if (blocks == 0) return hipSuccess;
-  pack_rows_tiled_kernel<T><<<(unsigned)blocks, 256, 0, stream>>>(src, ld, N, K, S, dst);
+  pack_rows_tiled_kernel<Src, T><<<(unsigned)blocks, 256, 0, stream>>>(src, ld, N, K, S, dst, rowmajor);
   return hipGetLastError();
+}
+
+// launch_pack_rows from a source in T, or in fp32 for a 2-byte T.
+template <class T>
+__host__ hipError_t pack_src(const void* src, int f32, int64_t ld, int rows, int K, int S, int64_t rows_pad, T* dst,
+                    hipStream_t stream, T* rowmajor = nullptr) {
+  if constexpr (sizeof(T) == 2) {
+    if (f32)
+      return launch_pack_rows<T, float>(static_cast<const float*>(src), ld, rows, K, S, rows_pad, dst, stream,
+                                        rowmajor);
+  }
+  return launch_pack_rows<T>(static_cast<const T*>(src), ld, rows, K, S, rows_pad, dst, stream, rowmajor);
 }
 
 // Loads of a KTile of R token rows (from n0, multiple of 32) from packed rows.

@@ -344,12 +344,12 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
       static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
       const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
   hipError_t e = hipGetLastError();
+  T* const hp = const_cast<T*>(static_cast<const T*>(p.hp));
+  T* const Wp = const_cast<T*>(static_cast<const T*>(p.Wp));
   if (e == hipSuccess)
-    e = launch_pack_rows<T>(static_cast<const T*>(p.h), p.ldh, p.N, p.K, plan.hS, plan.N_pad,
-                            const_cast<T*>(static_cast<const T*>(p.hp)), stream);
+    e = pack_src<T>(p.h, p.h_f32, p.ldh, p.N, p.K, plan.hS, plan.N_pad, hp, stream);
   if (e == hipSuccess)
-    e = launch_pack_rows<T>(static_cast<const T*>(p.W), p.ldw, p.V, p.K, plan.hS, plan.V_pad,
-                            const_cast<T*>(static_cast<const T*>(p.Wp)), stream);
+    e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream);
   timing_end(kKindPack, stream);
   return e;
 }

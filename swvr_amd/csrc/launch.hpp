@@ -44,6 +44,7 @@ struct FwdParams {
   const void* hp;      // h packed in its tiles' LDS image (pack_rows_tiled_kernel)
   const void* Wp;      // W packed the same way, [V_pad] rows
   int hS;              // reduction slices of both
+  int h_f32, w_f32;    // h / W stored in fp32 (rounded to the compute dtype as they are packed)
 };
 
 struct FwdPlan {
@@ -81,11 +82,13 @@ struct BwdPlan {
   int V_pad;             // vocabulary rows of the packed E / bias
   int hS;                // reduction slices of the packed h and W
   size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, off_Wp;
-  size_t off_flag, off_idx, off_inv, off_nact, off_delta, off_hc, ws_bytes;
+  size_t off_flag, off_idx, off_inv, off_nact, off_delta, off_hc, off_Wc, ws_bytes;
 };
 
+// w_f32: W is stored in fp32 and needs a row-major copy in the compute dtype
+// (the dh product reads W rows directly).
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
-              BwdPlan* plan);
+              BwdPlan* plan, bool w_f32 = false);
 
 struct BwdParams {
   const void* h;
@@ -109,6 +112,7 @@ struct BwdParams {
   int gE_dtype;
   float* gb;
   char* ws;
+  int h_f32, w_f32;    // h / W stored in fp32 (rounded to the compute dtype as they are read)
 };
 
 hipError_t bwd_launch(int dtype, const BwdPlan& plan, const BwdParams& p, hipStream_t stream);

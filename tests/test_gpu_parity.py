@@ -155,3 +155,29 @@ def test_gradients_are_deterministic():
     b = run(lambda *x: swvr.softmax_readout(*x, chunk_size=4096), inputs, gO, glse)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+def test_autocast_fp32_weights_round_while_packing_exactly_as_a_cast():
+    """Under autocast, fp32 h and W go to the kernels uncast (swvr_fwd_mixed / swvr_bwd_mixed):
+    the packing rounds them. The results must equal those of bf16 copies made beforehand, bit for
+    bit once the fp32 gradients are rounded to bf16 as the bf16 path writes them."""
+    N, K, V, D = 700, 256, 5003, 64
+    g = torch.Generator(device="cuda").manual_seed(0)
+    h = torch.randn(N, K, device="cuda", generator=g).requires_grad_(True)
+    W = (torch.randn(V, K, device="cuda", generator=g) * K ** -0.5).requires_grad_(True)
+    E = torch.randn(V, D, device="cuda", generator=g).requires_grad_(True)
+    b = (0.1 * torch.randn(V, device="cuda", generator=g)).requires_grad_(True)
+    gO = torch.randn(N, D, device="cuda", generator=g)
+    glse = torch.randn(N, device="cuda", generator=g)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        O, lse = swvr.softmax_readout(h, W, E, b, chunk_size=2048)
+    ga = torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), (h, W, E, b))
+    xs = [x.detach().to(torch.bfloat16).requires_grad_(True) for x in (h, W, E)]
+    bb = b.detach().clone().requires_grad_(True)
+    O2, lse2 = swvr.softmax_readout(*xs, bb, chunk_size=2048)
+    gb_ = torch.autograd.grad((O2 * gO).sum() + (lse2 * glse).sum(), (*xs, bb))
+    assert torch.equal(O, O2) and torch.equal(lse, lse2)
+    for a, r in zip(ga[:3], gb_[:3]):
+        assert a.dtype == torch.float32 and r.dtype == torch.bfloat16
+        assert torch.equal(a.to(torch.bfloat16), r)
+    assert torch.equal(ga[3], gb_[3])

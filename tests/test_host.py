@@ -88,6 +88,22 @@ def test_abi_combine_rejects_bad_arguments_without_touching_the_device():
                                 None, None, None, p, 1 << 20, None) == _lib.EINVAL
 
 
+def test_abi_mixed_storage_dtypes_are_checked():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    args = (4, 16, 8, 4, p, 16, p, 16, p, 4, None, 1.0, p, p, p, 1 << 20, None)
+    assert lib.swvr_fwd_mixed(_lib.BF16, _lib.F16, _lib.BF16, *args) == _lib.EDTYPE   # h in another 2-byte dtype
+    assert b"h dtype" in lib.swvr_last_error()
+    assert lib.swvr_fwd_mixed(_lib.F16, _lib.F16, _lib.BF16, *args) == _lib.EDTYPE
+    assert b"W dtype" in lib.swvr_last_error()
+    # an fp32 W adds its compute-dtype copy to the backward workspace
+    N, K, V, D = 1024, 512, 4096, 64
+    same = lib.swvr_bwd_workspace_size_mixed(_lib.BF16, _lib.BF16, N, K, V, D, 1024, 1)
+    f32w = lib.swvr_bwd_workspace_size_mixed(_lib.BF16, _lib.F32, N, K, V, D, 1024, 1)
+    assert same == lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 1024, 1)
+    assert f32w - same == V * K * 2
+
+
 def test_abi_bwd_rejects_bad_chunk_and_gradient_dtype():
     lib = _lib.load()
     p = ctypes.c_void_p(16)
