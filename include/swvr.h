@@ -150,6 +150,30 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
                    float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
+/* MSE readout loss over the forward's outputs, the loss of
+ * softmax_readout_mse (replaces swvr/api.py:53-66, which the reference
+ * evaluates as a chain of torch ops):
+ *   per_tok[n] = w[n] * (mean_d (O[n,d] - target[n,d])^2 + z_loss_weight * lse[n]^2)
+ * reduction SWVR_REDUCE_NONE writes per_tok into out [N]; SWVR_REDUCE_SUM
+ * writes sum_n per_tok[n] into out [1]; SWVR_REDUCE_MEAN writes that sum
+ * divided by sum_n w[n] (by N without weights).  The sum is taken in a fixed
+ * order, so it is the same on every run.  scale [1] (SUM / MEAN only;
+ * nullable) receives c, the factor the sum is multiplied by (1, 1/sum w or
+ * 1/N).  gO [N][D] and glse [N] (both or neither) receive the derivatives of
+ * the loss divided by c (and by the incoming gradient):
+ *   gO[n,d] = w[n] * (2/D) * (O[n,d] - target[n,d]),  glse[n] = w[n] * 2 z lse[n].
+ * O is dense fp32 [N][D]; target is [N][ldt] in target_dtype (SWVR_BF16,
+ * SWVR_F16 or SWVR_F32), unit column stride; weight is fp32 [N] or NULL.
+ * The workspace holds the per-workgroup partial sums
+ * (swvr_mse_loss_workspace_size; 0 bytes for SWVR_REDUCE_NONE is enough). */
+#define SWVR_REDUCE_NONE 0
+#define SWVR_REDUCE_SUM 1
+#define SWVR_REDUCE_MEAN 2
+size_t swvr_mse_loss_workspace_size(int64_t N);
+int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const void* target, int target_dtype,
+                  int64_t ldt, const float* weight, float z_loss_weight, int reduction, float* out, float* scale,
+                  float* gO, float* glse, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Instrumentation (no reference counterpart).  While enabled, every kernel
  * launch is bracketed by a pair of HIP events on its stream.
  * swvr_timing_collect synchronises those events, writes per-kernel-kind total

@@ -198,3 +198,82 @@ def softmax_readout_op(h2, W, E, bias, logit_scale, chunk, cdt):
         return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)
     with torch.autocast(h2.device.type, enabled=False):
         return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)
+
+
+# ---------------------------------------------------------------- fused MSE loss
+REDUCTIONS = {"none": 0, "sum": 1, "mean": 2}
+
+
+def _mse_loss(O, lse, target, weight, z, reduction, need_grad):
+    """Loss of swvr/api.py:53-66 over ``O`` [N, D] and ``lse`` [N] in one library call
+    (``swvr_mse_loss``): the output, the factor c of the reduction, and the loss's
+    derivatives divided by c (empty tensors when ``need_grad`` is false)."""
+    _require_device(O)
+    lib = _lib.load()
+    N, D = O.shape
+    O = O.contiguous()
+    lse = lse.contiguous()
+    t = target if target.dtype in _lib.DTYPE_TAG else target.to(torch.float32)
+    if t.stride(1) != 1 or (N > 1 and t.stride(0) < D):
+        t = t.contiguous()
+    w = weight.to(torch.float32).contiguous() if weight is not None else None
+    dev = O.device
+    out = torch.empty((N,) if reduction == 0 else (), dtype=torch.float32, device=dev)
+    scale = torch.empty((), dtype=torch.float32, device=dev)
+    gO = torch.empty_like(O) if need_grad else O.new_empty(0)
+    glse = torch.empty_like(lse) if need_grad else lse.new_empty(0)
+    ws_bytes = lib.swvr_mse_loss_workspace_size(N) if reduction else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.swvr_mse_loss(N, D, _lib.ptr(O), _lib.ptr(lse), _lib.ptr(t), _lib.DTYPE_TAG[t.dtype],
+                               t.stride(0) if N > 1 else D, _lib.ptr(w), float(z), int(reduction),
+                               _lib.ptr(out), _lib.ptr(scale) if reduction else None,
+                               _lib.ptr(gO) if need_grad else None, _lib.ptr(glse) if need_grad else None,
+                               _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
+    _lib.check(rc)
+    if not reduction:
+        scale.fill_(1.0)
+    return out, scale, gO, glse
+
+
+@torch.library.custom_op("swvr::mse_loss", mutates_args=())
+def _mse_op(O: torch.Tensor, lse: torch.Tensor, target: torch.Tensor, weight: Optional[torch.Tensor],
+            z: float, reduction: int, need_grad: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                torch.Tensor]:
+    return _mse_loss(O, lse, target, weight, z, reduction, need_grad)
+
+
+@_mse_op.register_fake
+def _(O, lse, target, weight, z, reduction, need_grad):
+    N = O.shape[0]
+    out = O.new_empty((N,) if reduction == 0 else ())
+    gO = O.new_empty(O.shape) if need_grad else O.new_empty(0)
+    glse = lse.new_empty(lse.shape) if need_grad else lse.new_empty(0)
+    return out, O.new_empty(()), gO, glse
+
+
+def _mse_setup_context(ctx, inputs, output):
+    reduction = inputs[5]
+    _, scale, gO, glse = output
+    ctx.mark_non_differentiable(scale, gO, glse)
+    ctx.save_for_backward(scale, gO, glse)
+    ctx.reduction = reduction
+
+
+def _mse_autograd_backward(ctx, g, _g_scale, _g_gO, _g_glse):
+    scale, gO, glse = ctx.saved_tensors
+    if ctx.reduction == 0:
+        return gO * g[:, None], glse * g, None, None, None, None, None
+    s = g * scale
+    return gO * s, glse * s, None, None, None, None, None
+
+
+_mse_op.register_autograd(_mse_autograd_backward, setup_context=_mse_setup_context)
+
+
+def mse_loss_op(O2, lse, target2, weight, z_loss_weight, reduction):
+    """Fused loss over ``O2`` [N, D] and ``lse`` [N] (swvr/api.py:53-66); ``reduction`` is
+    "none", "sum" or "mean".  Returns the loss ([N] for "none", else a scalar)."""
+    need_grad = torch.is_grad_enabled() and (O2.requires_grad or lse.requires_grad)
+    out, _, _, _ = _mse_op(O2, lse, target2, weight, float(z_loss_weight), REDUCTIONS[reduction], need_grad)
+    return out

@@ -10,7 +10,7 @@ import os
 import torch
 from torch import nn
 
-from ._ops import DEFAULT_CHUNK, softmax_readout_op
+from ._ops import DEFAULT_CHUNK, REDUCTIONS, mse_loss_op, softmax_readout_op
 
 
 def default_chunk_size():
@@ -67,6 +67,11 @@ def softmax_readout_mse(h, W, E, target, bias=None, *, weight=None, reduction="m
     ``"none"`` are also accepted.
     """
     O, lse = softmax_readout(h, W, E, bias, logit_scale=logit_scale, chunk_size=chunk_size)
+    if _fusable_loss(O, lse, target, weight, reduction):
+        D = O.shape[-1]
+        out = mse_loss_op(O.reshape(-1, D), lse.reshape(-1), target.reshape(-1, D),
+                          weight.reshape(-1) if weight is not None else None, z_loss_weight, reduction)
+        return out.view(lse.shape) if reduction == "none" else out
     per_tok = (O - target.to(O.dtype)).pow(2).mean(dim=-1)
     if z_loss_weight:
         per_tok = per_tok + z_loss_weight * lse.pow(2)
@@ -80,6 +85,25 @@ def softmax_readout_mse(h, W, E, target, bias=None, *, weight=None, reduction="m
         denom = weight.to(per_tok.dtype).sum() if weight is not None else per_tok.numel()
         return per_tok.sum() / denom
     raise ValueError(f"unknown reduction {reduction!r}")
+
+
+def _fusable_loss(O, lse, target, weight, reduction):
+    """The library's loss kernels (``swvr::mse_loss``) compute the loss when the target and the
+    weight have exactly the token shapes, live on O's device and need no gradient of their own;
+    anything else (broadcasting, a differentiable target, an unknown reduction) takes the
+    composite formula, which keeps the reference's semantics and errors."""
+    if reduction not in REDUCTIONS or O.device.type != "cuda" or O.shape[-1] < 1 or lse.numel() == 0:
+        return False
+    if not isinstance(target, torch.Tensor) or target.shape != O.shape or target.device != O.device:
+        return False
+    if target.requires_grad or target.is_complex():
+        return False
+    if weight is not None:
+        if not isinstance(weight, torch.Tensor) or weight.shape != lse.shape or weight.device != O.device:
+            return False
+        if weight.requires_grad or weight.is_complex():
+            return False
+    return True
 
 
 def _weight_of(x):

@@ -52,7 +52,8 @@ hipEvent_t take_event() {
 
 const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
-                                     "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel"};
+                                     "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel",
+                                     "mse_loss"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 
@@ -312,6 +313,49 @@ int swvr_timing_collect(double* total_ms, int64_t* launches, int max_kinds) {
     if (launches) launches[k] = cnt[k];
   }
   return kNumKinds;
+}
+
+size_t swvr_mse_loss_workspace_size(int64_t N) {
+  if (N < 0 || N > INT32_MAX) return 0;
+  return swvr::mse_workspace_bytes((int)N);
+}
+
+int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const void* target, int target_dtype,
+                  int64_t ldt, const float* weight, float z_loss_weight, int reduction, float* out, float* scale,
+                  float* gO, float* glse, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (N < 0 || D < 1) return fail(SWVR_EINVAL, "bad sizes N=%lld D=%lld", (long long)N, (long long)D);
+  if (N > INT32_MAX || D > INT32_MAX || N * D > ((int64_t)1 << 40)) return fail(SWVR_EINVAL, "sizes too large");
+  if (!is_dtype(target_dtype)) return fail(SWVR_EDTYPE, "unsupported target dtype tag %d", target_dtype);
+  if (reduction < SWVR_REDUCE_NONE || reduction > SWVR_REDUCE_MEAN)
+    return fail(SWVR_EINVAL, "unknown reduction %d", reduction);
+  if (ldt < D) return fail(SWVR_EINVAL, "ldt=%lld must be >= D", (long long)ldt);
+  if (!out) return fail(SWVR_EINVAL, "out must be non-null");
+  if ((gO == nullptr) != (glse == nullptr)) return fail(SWVR_EINVAL, "gO and glse must both be given or both NULL");
+  if (N > 0 && (!O || !lse || !target)) return fail(SWVR_EINVAL, "O, lse and target must be non-null");
+  const size_t need = reduction == SWVR_REDUCE_NONE ? 0 : swvr::mse_workspace_bytes((int)N);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(SWVR_EWORKSPACE, "loss workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reduction == SWVR_REDUCE_NONE && N == 0) return SWVR_OK;
+  swvr::MseParams p{};
+  p.O = O;
+  p.lse = lse;
+  p.target = target;
+  p.ldt = ldt;
+  p.target_dtype = target_dtype;
+  p.weight = weight;
+  p.N = (int)N;
+  p.D = (int)D;
+  p.z = z_loss_weight;
+  p.reduce = reduction;
+  p.per_tok = reduction == SWVR_REDUCE_NONE ? out : nullptr;
+  p.out = reduction == SWVR_REDUCE_NONE ? nullptr : out;
+  p.scale = scale;
+  p.gO = gO;
+  p.glse = glse;
+  hipError_t e = swvr::mse_launch(p, workspace, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "loss launch");
+  return SWVR_OK;
 }
 
 const char* swvr_kernel_name(int kind) {

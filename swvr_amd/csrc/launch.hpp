@@ -17,6 +17,7 @@ enum KernelKind {
   kKindFill,
   kKindPack,
   kKindBwdExpand,
+  kKindLoss,
   kNumKinds
 };
 
@@ -116,5 +117,25 @@ struct BwdParams {
 };
 
 hipError_t bwd_launch(int dtype, const BwdPlan& plan, const BwdParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- MSE loss
+struct MseParams {
+  const float* O;       // [N][D] fp32
+  const float* lse;     // [N] fp32
+  const void* target;   // [N][ldt], target_dtype (0 bf16, 1 f16, 2 f32)
+  int64_t ldt;
+  int target_dtype;
+  const float* weight;  // [N] fp32 or null
+  int N, D;
+  float z;              // z-loss weight
+  int reduce;           // 0 none, 1 sum, 2 mean
+  float* per_tok;       // [N] (reduce == 0) or null
+  float* out;           // [1] (reduce != 0)
+  float* scale;         // [1] (reduce != 0): the c of the loss
+  float* gO;            // [N][D] or null
+  float* glse;          // [N] or null (with gO)
+};
+size_t mse_workspace_bytes(int N);
+hipError_t mse_launch(const MseParams& p, void* ws, hipStream_t stream);
 
 }  // namespace swvr

@@ -197,3 +197,22 @@ def test_default_chunk_size_env(monkeypatch):
     assert swvr_amd.default_chunk_size() == 8192
     monkeypatch.setenv("SWVR_CHUNK", "4096")
     assert swvr_amd.default_chunk_size() == 4096
+
+
+def test_abi_loss_rejects_bad_arguments_without_touching_the_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    ws = lib.swvr_mse_loss_workspace_size(100)
+    assert ws == 2 * 7 * 4  # two fp32 partial sums per 16-token workgroup
+
+    def call(N=100, D=8, tdt=_lib.F32, ldt=8, red=2, out=p, gO=None, glse=None, wsb=ws, wsp=p):
+        return lib.swvr_mse_loss(N, D, p, p, p, tdt, ldt, None, 0.0, red, out, None, gO, glse, wsp, wsb, None)
+
+    assert call(D=0) == _lib.EINVAL
+    assert call(tdt=7) == _lib.EDTYPE
+    assert call(red=3) == _lib.EINVAL and b"reduction" in lib.swvr_last_error()
+    assert call(ldt=4) == _lib.EINVAL and b"ldt" in lib.swvr_last_error()
+    assert call(out=None) == _lib.EINVAL
+    assert call(gO=p) == _lib.EINVAL and b"both" in lib.swvr_last_error()
+    assert call(wsb=ws - 4) == _lib.EWORKSPACE
+    assert call(N=0, red=0, wsb=0, wsp=None) == _lib.OK  # no tokens, no reduction: nothing to do
