@@ -150,6 +150,20 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
                    float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Forward with h and W in OCP e4m3 (fp8; opt-in, outside the reference's
+ * precision policy, which has no fp8 path).  h [N][ldh] and W [V][ldw] hold
+ * e4m3 bytes: h = h_scale[0] * h_e4m3 and W[v] = w_scale[v] * W_e4m3[v]
+ * (fp32 scales on the device: one for h, one per vocabulary row of W).  The
+ * scores S = logit_scale * h_scale * w_scale[v] * (h_e4m3 . W_e4m3[v]) + bias
+ * accumulate in fp32; P is rounded to bf16 for P.E as in the bf16 forward; E
+ * is bf16 [V][lde]; O and lse are fp32.  K, ldh and ldw are multiples of 16
+ * (bytes), h and W 16-byte aligned; D <= 128.  There is no e4m3 backward:
+ * gradients come from swvr_bwd on bf16 operands. */
+size_t swvr_fwd_fp8_workspace_size(int64_t N, int64_t K, int64_t V, int64_t D);
+int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const float* h_scale,
+                 const void* W, int64_t ldw, const float* w_scale, const void* E, int64_t lde, const float* bias,
+                 float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
 /* MSE readout loss over the forward's outputs, the loss of
  * softmax_readout_mse (replaces swvr/api.py:53-66, which the reference
  * evaluates as a chain of torch ops):

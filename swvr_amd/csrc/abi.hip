@@ -127,7 +127,7 @@ int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_
   if (N == 0) return SWVR_OK;
   if (!workspace || workspace_bytes < plan.ws_bytes)
     return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
-  FwdParams p;
+  FwdParams p{};
   p.h = h;
   p.ldh = ldh;
   p.W = W;
@@ -313,6 +313,52 @@ int swvr_timing_collect(double* total_ms, int64_t* launches, int max_kinds) {
     if (launches) launches[k] = cnt[k];
   }
   return kNumKinds;
+}
+
+size_t swvr_fwd_fp8_workspace_size(int64_t N, int64_t K, int64_t V, int64_t D) {
+  if (N < 0 || K < 0 || V < 0 || D < 0 || K % 16 != 0 || N > INT32_MAX || V > INT32_MAX) return 0;
+  FwdPlan plan;
+  if (!fwd_plan(kFwdFP8, N, K / 2, V, D, &plan)) return 0;
+  return plan.ws_bytes;
+}
+
+int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const float* h_scale,
+                 const void* W, int64_t ldw, const float* w_scale, const void* E, int64_t lde, const float* bias,
+                 float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (D > 128) return fail(SWVR_EDTYPE, "D=%lld exceeds the maximum 128 of the e4m3 forward", (long long)D);
+  if (K % 16 != 0 || ldh % 16 != 0 || ldw % 16 != 0)
+    return fail(SWVR_EINVAL, "K=%lld, ldh=%lld and ldw=%lld must be multiples of 16 (e4m3 bytes)", (long long)K,
+                (long long)ldh, (long long)ldw);
+  // the e4m3 rows travel as bf16 rows of K / 2 elements
+  int rc = check_common(SWVR_BF16, N, K / 2, V, D, h, ldh / 2, W, ldw / 2, E, lde);
+  if (rc != SWVR_OK) return rc;
+  if (N > 0 && (!O || !lse)) return fail(SWVR_EINVAL, "O and lse must be non-null");
+  if (N > 0 && V > 0 && (!h_scale || !w_scale)) return fail(SWVR_EINVAL, "h_scale and w_scale must be non-null");
+  FwdPlan plan;
+  if (!fwd_plan(kFwdFP8, N, K / 2, V, D, &plan)) return fail(SWVR_EDTYPE, "no e4m3 forward kernel for D=%lld", (long long)D);
+  if (N == 0) return SWVR_OK;
+  if (!workspace || workspace_bytes < plan.ws_bytes)
+    return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+  FwdParams p{};
+  p.h = h;
+  p.ldh = ldh / 2;
+  p.W = W;
+  p.ldw = ldw / 2;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)(K / 2);
+  p.V = (int)V;
+  p.D = (int)D;
+  p.h_scale = h_scale;
+  p.w_scale = w_scale;
+  hipError_t e = fwd_launch(kFwdFP8, plan, p, static_cast<char*>(workspace), O, lse, nullptr, nullptr,
+                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return SWVR_OK;
 }
 
 size_t swvr_mse_loss_workspace_size(int64_t N) {

@@ -28,7 +28,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(float)))) float f32x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
-enum { kBF16 = 0, kF16 = 1, kF32 = 2 };
+enum { kBF16 = 0, kF16 = 1, kF32 = 2, kFP8 = 3 };  // kFP8: h, W in OCP e4m3; E in bf16
 
 template <class T> struct Vec8;
 template <> struct Vec8<bf16_t> { typedef bf16x8_t type; };
@@ -706,6 +706,52 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
       cur = nxt;
     }
     mma_step(acc, cur);
+  }
+}
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// 32 bytes of e4m3 operand from two 16-byte reads.
+__device__ __forceinline__ i32x8_t cat16(bf16x8_t lo, bf16x8_t hi) {
+  const i32x4_t l = __builtin_bit_cast(i32x4_t, lo), h = __builtin_bit_cast(i32x4_t, hi);
+  return __builtin_shufflevector(l, h, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// c += a b over 64 k-values, e4m3 x e4m3 -> fp32 (v_mfma_f32_32x32x64_f8f6f4;
+// format code 0 = e4m3 for both operands, no block scales).
+__device__ __forceinline__ void mfma_f8_k64(f32x16_t& c, i32x8_t a, i32x8_t b) {
+  c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// tile_reduce for e4m3 operands packed as if they were bf16 pairs: a staged
+// 64-byte row slice holds 64 k-values, and one k64 MFMA consumes it.  Each
+// lane's 32 operand bytes are the two 16-byte pieces the bf16 reduction reads
+// for its two k16 steps (bytes 16 hi .. 16 hi + 15 and 32 + 16 hi .. 32 + 16 hi
+// + 15 of the slice, hi = lane / 32).  A and B take the same bytes per lane, so
+// whatever order the instruction gives the k-values inside its 64, every
+// product pairs h[n, k] with W[v, k] of the same k.
+template <int L, int FM, int FN, class TA, class TB, class R, class F>
+__device__ __forceinline__ void tile_reduce_f8(f32x16_t (&acc)[FM][FN], const TA&, const TB&, const char* smem,
+                                               int sb, R& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
+  OpOffsets<typename TA::Layout, FM, 2> ao;
+  ao.init(a_row0);
+  OpOffsets<typename TB::Layout, FN, 2> bo;
+  bo.init(b_row0);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt > 0) ring.template publish_next<L>();
+    const char* sA = smem + ring.slot * sb;
+    const char* sB = sA + TA::BYTES;
+    issue_next();
+    i32x8_t b[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) b[fn] = cat16(bo.read(sB, 0, fn), bo.read(sB, 1, fn));
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const i32x8_t a = cat16(ao.read(sA, 0, fm), ao.read(sA, 1, fm));
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[fm][fn], a, b[fn]);
+    }
   }
 }
 

@@ -15,6 +15,8 @@
 //     feeds acc^T += E^T P^T straight from the score registers;
 //   * partials (m, l, acc) of all waves and splits are merged by
 //     fwd_combine_kernel in a fixed order (deterministic).
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -40,14 +42,35 @@ struct FwdTile {
   static constexpr int NS = narrow ? 3 : kStages;  // LDS ring depth
 };
 
+// The e4m3 forward (h and W in OCP e4m3, E and P in bf16): one k64 MFMA per
+// 64-byte slice takes 32 operand bytes per lane, twice the bf16 k16 step's, so
+// each wave owns 128 vocabulary rows x 32 tokens (the 128 x 64 wave of the
+// bf16 tile would not fit its accumulators and operands in 256 registers).
+static_assert(kFP8 == kFwdFP8, "one dtype code for the e4m3 forward");
+
+template <int DP>
+struct FwdTileF8 {
+  static constexpr int BV = 256, BM = 128, WV = 2, WT = 4;
+  static constexpr int NT = 64 * WV * WT;
+  static constexpr int NS = 3;
+};
+
+template <class T, int DP, bool F8>
+using FwdCfg = typename std::conditional<F8, FwdTileF8<DP>, FwdTile<T, DP>>::type;
+
 // Vocabulary operands of the forward, packed once per call: E^T per
 // vocabulary tile as [n_vt][DP][BV] (compute dtype; column p of tile vt is
 // row vt * BV + pe_row(p) of E; zero past D and V) and the bias as fp32
 // [V_pad] (-inf past V: padding rows drop out of the softmax).
+// With w_scale set (the e4m3 forward) the bias goes out as (bias, multiplier)
+// pairs, multiplier = logit_scale * h_scale * w_scale[v] (0 past V): the
+// factor that turns the e4m3 dot product into a score.
 template <class T>
 __global__ __launch_bounds__(256) void pack_et_kernel(const T* __restrict__ E, int64_t lde,
                                                       const float* __restrict__ bias, int V, int D, int V_pad,
-                                                      int DP, int BV, T* __restrict__ Et, float* __restrict__ biasp) {
+                                                      int DP, int BV, T* __restrict__ Et, float* __restrict__ biasp,
+                                                      const float* __restrict__ h_scale,
+                                                      const float* __restrict__ w_scale, float logit_scale) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e < (int64_t)V_pad * DP) {
     const int64_t tile = e / ((int64_t)DP * BV);
@@ -56,13 +79,21 @@ __global__ __launch_bounds__(256) void pack_et_kernel(const T* __restrict__ E, i
     const int64_t v = tile * BV + pe_row(p);
     Et[e] = (v < V && d < D) ? E[v * lde + d] : (T)0.f;
   }
-  if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
+  if (e < V_pad) {
+    const float b = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
+    if (w_scale) {
+      biasp[2 * e] = b;
+      biasp[2 * e + 1] = e < V ? logit_scale * h_scale[0] * w_scale[e] : 0.f;
+    } else {
+      biasp[e] = b;
+    }
+  }
 }
 
 
-template <class T, int DP>
-__global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParams p) {
-  typedef FwdTile<T, DP> C;
+template <class T, int DP, bool F8 = false>
+__global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdParams p) {
+  typedef FwdCfg<T, DP, F8> C;
   typedef typename Vec8<T>::type V8;
   constexpr int kBK = SliceK<T>::value;
   constexpr int BV = C::BV, BM = C::BM, NT = C::NT;
@@ -75,7 +106,7 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
   constexpr int FV = WVR / 32, FT = WTR / 32;  // 32x32 blocks per wave
   constexpr int DB = DP / 32;
   constexpr int EBYTES = TE::BYTES;
-  constexpr int BBYTES = BV * 4;
+  constexpr int BBYTES = BV * 4 * (F8 ? 2 : 1);  // bias, or (bias, multiplier) pairs
 
   constexpr int NS = C::NS;
   __shared__ __attribute__((aligned(1024))) char smem[NS * SB + EBYTES + BBYTES];
@@ -140,13 +171,17 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
       TE te;
       te.setup(Ep + (int64_t)v0 * DP, BV, DP, BV);
       te.issue(ldsE, 0);
-      if ((int)threadIdx.x * 16 < BBYTES) dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
+      if ((int)threadIdx.x * 16 < BBYTES)
+        dma_batch1(make_rsrc(p.biasp + (int64_t)v0 * (F8 ? 2 : 1)), (uint32_t)threadIdx.x * 16, ldsB + w * 1024);
     }
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
-    tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
+    if constexpr (F8)
+      tile_reduce_f8<L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
+    else
+      tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
     if (nk < NS) {
       // short reduction: the E / bias loads may still be in flight
       wait_vmcnt<0>();
@@ -162,13 +197,23 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_tile_kernel(FwdParam
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // registers 4g..4g+3 hold rows 8g + 4(lane/32) + 0..3 of the block
-        const float4 b4 = *reinterpret_cast<const float4*>(sBias + wv * WVR + fv * 32 + 8 * g + (lane >> 5) * 4);
-        const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+        const int row = wv * WVR + fv * 32 + 8 * g + (lane >> 5) * 4;
+        float bb[4], mm[4];
+        if constexpr (F8) {
+          const float4 x0 = *reinterpret_cast<const float4*>(sBias + 2 * row);
+          const float4 x1 = *reinterpret_cast<const float4*>(sBias + 2 * row + 4);
+          bb[0] = x0.x; mm[0] = x0.y; bb[1] = x0.z; mm[1] = x0.w;
+          bb[2] = x1.x; mm[2] = x1.y; bb[3] = x1.z; mm[3] = x1.w;
+        } else {
+          const float4 b4 = *reinterpret_cast<const float4*>(sBias + row);
+          bb[0] = b4.x; bb[1] = b4.y; bb[2] = b4.z; bb[3] = b4.w;
+          mm[0] = mm[1] = mm[2] = mm[3] = p.scale;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int ft = 0; ft < FT; ++ft) {
-            const float x = fmaf(sacc[fv][ft][4 * g + i], p.scale, bb[i]);  // rounded as the backward rounds it
+            const float x = fmaf(sacc[fv][ft][4 * g + i], mm[i], bb[i]);  // rounded as the backward rounds it
             sacc[fv][ft][4 * g + i] = x;
             mx[ft] = fmaxf(mx[ft], x);
           }
@@ -293,13 +338,13 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   }
 }
 
-template <class T, int DP>
+template <class T, int DP, bool F8 = false>
 hipError_t launch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
-  typedef FwdTile<T, DP> C;
+  typedef FwdCfg<T, DP, F8> C;
   if (plan.BV != C::BV || plan.BM != C::BM) return hipErrorInvalidValue;
   const int blocks = plan.n_tb * plan.n_split;
   timing_begin(kKindFwdTile, stream);
-  fwd_tile_kernel<T, DP><<<blocks, C::NT, 0, stream>>>(p);
+  fwd_tile_kernel<T, DP, F8><<<blocks, C::NT, 0, stream>>>(p);
   timing_end(kKindFwdTile, stream);
   return hipGetLastError();
 }
@@ -313,6 +358,15 @@ hipError_t dispatch_dp(const FwdPlan& plan, const FwdParams& p, hipStream_t stre
     case 256:
       if constexpr (sizeof(T) == 2) return launch_tile<T, 256>(plan, p, stream);
       return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t dispatch_dp_f8(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
+  switch (plan.DP) {
+    case 32: return launch_tile<bf16_t, 32, true>(plan, p, stream);
+    case 64: return launch_tile<bf16_t, 64, true>(plan, p, stream);
+    case 128: return launch_tile<bf16_t, 128, true>(plan, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -342,7 +396,7 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   timing_begin(kKindPack, stream);
   pack_et_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
       static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
-      const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp));
+      const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp), p.h_scale, p.w_scale, p.scale);
   hipError_t e = hipGetLastError();
   T* const hp = const_cast<T*>(static_cast<const T*>(p.hp));
   T* const Wp = const_cast<T*>(static_cast<const T*>(p.Wp));
@@ -368,6 +422,13 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
     tbytes = 4;
   } else if (dtype == kBF16 || dtype == kF16) {
     tile_of<bf16_t>(DP, &BV, &BM, &WV);
+    tbytes = 2;
+  } else if (dtype == kFP8) {
+    // K counts byte pairs: the e4m3 rows are packed as bf16 rows of K / 2 elements
+    if (DP > 128) return false;
+    BV = FwdTileF8<64>::BV;
+    BM = FwdTileF8<64>::BM;
+    WV = FwdTileF8<64>::WV;
     tbytes = 2;
   } else {
     return false;
@@ -400,7 +461,7 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   plan->off_Ep = off;
   off += align256((size_t)plan->V_pad * DP * tbytes);
   plan->off_bias = off;
-  off += align256((size_t)plan->V_pad * 4);
+  off += align256((size_t)plan->V_pad * 4 * (dtype == kFP8 ? 2 : 1));
   plan->N_pad = ((N + 255) / 256) * 256;
   plan->hS = packed_slices(K, tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value);
   plan->off_hp = off;
@@ -430,6 +491,7 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
     case kBF16: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, p, stream); break;
     case kF16: e = pack<f16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<f16_t>(plan, p, stream); break;
     case kF32: e = pack<float>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<float>(plan, p, stream); break;
+    case kFP8: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp_f8(plan, p, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;

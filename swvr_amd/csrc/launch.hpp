@@ -46,6 +46,8 @@ struct FwdParams {
   const void* Wp;      // W packed the same way, [V_pad] rows
   int hS;              // reduction slices of both
   int h_f32, w_f32;    // h / W stored in fp32 (rounded to the compute dtype as they are packed)
+  const float* h_scale;  // e4m3 forward: [1] dequantisation scale of h, else null
+  const float* w_scale;  // e4m3 forward: [V] dequantisation scales of W's rows, else null
 };
 
 struct FwdPlan {
@@ -56,6 +58,9 @@ struct FwdPlan {
   int hS;                // reduction slices of the packed h and W
   size_t off_m, off_l, off_acc, off_Ep, off_bias, off_hp, off_Wp, ws_bytes;
 };
+
+// fwd_plan / fwd_launch dtype of the e4m3 forward (h, W in e4m3; E in bf16).
+constexpr int kFwdFP8 = 3;
 
 // Tile shape, split count and workspace for a forward call; ok=false if the
 // dtype / D combination is unsupported.

@@ -1,0 +1,80 @@
+"""The opt-in e4m3 forward (``swvr_fwd_fp8`` behind ``swvr_amd.fp8``).
+
+The reference has no fp8 path, so there is nothing of its to match: the
+kernel is held to the fp64 oracle evaluated on the dequantised operands (the
+values it computes with) at the bf16 forward's tolerance, and to the
+unquantised readout at a tolerance for e4m3 rounding of h and W.
+"""
+import pytest
+import torch
+
+from oracle import reference as ref
+from swvr_amd import fp8
+from tests.gpu_util import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def make(N, K, V, D, seed=0, bias=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    h = torch.randn(N, K, device="cuda", generator=g)
+    W = torch.randn(V, K, device="cuda", generator=g) / K ** 0.5
+    E = torch.randn(V, D, device="cuda", generator=g).to(torch.bfloat16)
+    b = 0.5 * torch.randn(V, device="cuda", generator=g) if bias else None
+    return h, W, E, b
+
+
+def oracle(h, W, E, b, logit_scale):
+    O, lse = ref.softmax_readout_reference(h.double().cpu(), W.double().cpu(), E.double().cpu(),
+                                           b.double().cpu() if b is not None else None, logit_scale)
+    return O, lse
+
+
+@pytest.mark.parametrize("N,K,V,D", [(300, 512, 4099, 64), (1, 64, 1000, 5), (1000, 80, 2500, 128),
+                                     (517, 2560, 8192, 32), (256, 16, 300, 64)])
+@pytest.mark.parametrize("bias", [True, False])
+def test_fp8_forward_matches_fp64_on_the_dequantised_operands(N, K, V, D, bias):
+    h, W, E, b = make(N, K, V, D, bias=bias)
+    O, lse = fp8.softmax_readout_fp8(h, W, E, b, logit_scale=0.7)
+    hq, hs = fp8.quantize_tensor(h)
+    Wq, ws = fp8.quantize_rows(W)
+    Or, lr = oracle(fp8.dequantize(hq, hs), fp8.dequantize(Wq, ws), E, b, 0.7)
+    eo, el = rel_err(O, Or), rel_err(lse, lr)
+    print(N, K, V, D, bias, f"vs dequantised: O {eo:.1e} lse {el:.1e}")
+    assert O.shape == (N, D) and lse.shape == (N,)
+    assert eo <= 1e-2 and el <= 1e-5
+
+
+@pytest.mark.parametrize("K", [512, 2560])
+def test_fp8_forward_stays_within_e4m3_rounding_of_the_unquantised_readout(K):
+    N, V, D = 512, 8192, 64
+    h, W, E, b = make(N, K, V, D, seed=1)
+    O, lse = fp8.softmax_readout_fp8(h, W, E, b)
+    Or, lr = oracle(h, W, E, b, 1.0)
+    eo, el = rel_err(O, Or), (lse.double().cpu() - lr).abs().max().item()
+    print(K, f"vs unquantised: O {eo:.2e}, lse max abs {el:.2e}")
+    assert eo <= 0.1 and el <= 0.1
+
+
+def test_fp8_masks_leading_dims_and_reuse_of_a_quantised_W():
+    N, K, V, D = 240, 128, 3000, 16
+    h, W, E, b = make(N, K, V, D, seed=2)
+    b[::3] = float("-inf")  # masked vocabulary rows
+    h3 = h.reshape(4, 60, K)
+    O, lse = fp8.softmax_readout_fp8(h3, W, E, b)
+    assert O.shape == (4, 60, D) and lse.shape == (4, 60)
+    O2, lse2 = fp8.softmax_readout_fp8(h3, W, E, b, w_q=fp8.quantize_rows(W))
+    assert torch.equal(O, O2) and torch.equal(lse, lse2)   # deterministic, same quantisation
+    hq, hs = fp8.quantize_tensor(h)
+    Wq, ws = fp8.quantize_rows(W)
+    Or, lr = oracle(fp8.dequantize(hq, hs), fp8.dequantize(Wq, ws), E, b, 1.0)
+    assert rel_err(O.reshape(N, D), Or) <= 1e-2 and rel_err(lse.reshape(N), lr) <= 1e-5
+
+
+def test_fp8_is_forward_only_and_caps_D():
+    h, W, E, b = make(64, 64, 500, 8)
+    with pytest.raises(RuntimeError, match="forward only"):
+        fp8.softmax_readout_fp8(h.requires_grad_(True), W, E, b)
+    h, W, E, b = make(64, 64, 500, 200)
+    with pytest.raises(NotImplementedError):
+        fp8.softmax_readout_fp8(h, W, E, b)

@@ -216,3 +216,19 @@ def test_abi_loss_rejects_bad_arguments_without_touching_the_device():
     assert call(gO=p) == _lib.EINVAL and b"both" in lib.swvr_last_error()
     assert call(wsb=ws - 4) == _lib.EWORKSPACE
     assert call(N=0, red=0, wsb=0, wsp=None) == _lib.OK  # no tokens, no reduction: nothing to do
+
+
+def test_abi_fp8_forward_checks_arguments_without_touching_the_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    assert lib.swvr_fwd_fp8_workspace_size(100, 64, 1000, 64) > 0
+    assert lib.swvr_fwd_fp8_workspace_size(100, 40, 1000, 64) == 0     # K not a multiple of 16
+    assert lib.swvr_fwd_fp8_workspace_size(100, 64, 1000, 200) == 0    # D above 128
+
+    def call(K=64, ldh=64, ldw=64, D=16, hs=p, ws=p):
+        return lib.swvr_fwd_fp8(8, K, 40, D, p, ldh, hs, p, ldw, ws, p, D, None, 1.0, p, p, p, 1 << 20, None)
+
+    assert call(K=40, ldh=40, ldw=40) == _lib.EINVAL
+    assert call(ldh=72) == _lib.EINVAL          # leading dim not a multiple of 16
+    assert call(D=200) == _lib.EDTYPE
+    assert call(hs=None) == _lib.EINVAL and b"scale" in lib.swvr_last_error()
