@@ -164,6 +164,18 @@ int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int6
                  const void* W, int64_t ldw, const float* w_scale, const void* E, int64_t lde, const float* bias,
                  float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
+/* OCP e4m3 quantisation of h or W for swvr_fwd_fp8 (no reference
+ * counterpart).  x is [R][ld] in x_dtype (SWVR_BF16, SWVR_F16, SWVR_F32);
+ * out receives [R][ldo] e4m3 bytes (16-byte aligned, ldo a multiple of 16),
+ * columns K .. Kp-1 zero.  per_row != 0: scale[r] = max(amax of row r, 1e-30)
+ * * fl(1/448) (W); per_row == 0: one scale[0] from the amax of the whole
+ * matrix (h), which needs swvr_quantize_e4m3_workspace_size(R, 0) bytes of
+ * workspace.  out = x / scale rounded to nearest even: the same bytes and
+ * scales as torch's (x / (amax.clamp_min(1e-30) / 448)).to(float8_e4m3fn). */
+size_t swvr_quantize_e4m3_workspace_size(int64_t R, int per_row);
+int swvr_quantize_e4m3(int64_t R, int64_t K, int64_t Kp, const void* x, int64_t ld, int x_dtype, int per_row,
+                       void* out, int64_t ldo, float* scale, void* workspace, size_t workspace_bytes, void* stream);
+
 /* MSE readout loss over the forward's outputs, the loss of
  * softmax_readout_mse (replaces swvr/api.py:53-66, which the reference
  * evaluates as a chain of torch ops):

@@ -53,7 +53,7 @@ hipEvent_t take_event() {
 const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
                                      "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel",
-                                     "mse_loss"};
+                                     "mse_loss",          "quantize_e4m3"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 
@@ -358,6 +358,43 @@ int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int6
   hipError_t e = fwd_launch(kFwdFP8, plan, p, static_cast<char*>(workspace), O, lse, nullptr, nullptr,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return SWVR_OK;
+}
+
+size_t swvr_quantize_e4m3_workspace_size(int64_t R, int per_row) {
+  if (R < 0 || R > INT32_MAX) return 0;
+  return per_row ? 0 : (size_t)R * sizeof(float);
+}
+
+int swvr_quantize_e4m3(int64_t R, int64_t K, int64_t Kp, const void* x, int64_t ld, int x_dtype, int per_row,
+                       void* out, int64_t ldo, float* scale, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (R < 0 || K < 0 || Kp < K || R > INT32_MAX || Kp > INT32_MAX)
+    return fail(SWVR_EINVAL, "bad sizes R=%lld K=%lld Kp=%lld", (long long)R, (long long)K, (long long)Kp);
+  if (Kp % 16 != 0) return fail(SWVR_EINVAL, "Kp=%lld must be a multiple of 16", (long long)Kp);
+  if (!is_dtype(x_dtype)) return fail(SWVR_EDTYPE, "unsupported input dtype tag %d", x_dtype);
+  if (ld < K || ldo < Kp || ldo % 16 != 0)
+    return fail(SWVR_EINVAL, "ld=%lld must be >= K, ldo=%lld >= Kp and a multiple of 16", (long long)ld,
+                (long long)ldo);
+  if (R == 0) return SWVR_OK;
+  if ((K > 0 && !x) || !out || !scale || !aligned16(out)) return fail(SWVR_EINVAL, "x, out (16-byte aligned) and scale must be non-null");
+  const size_t need = swvr_quantize_e4m3_workspace_size(R, per_row);
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(SWVR_EWORKSPACE, "quantisation workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  swvr::QuantParams q{};
+  q.x = x;
+  q.ld = ld;
+  q.x_dtype = x_dtype;
+  q.R = (int)R;
+  q.K = (int)K;
+  q.Kp = (int)Kp;
+  q.per_row = per_row != 0;
+  q.out = out;
+  q.ldo = ldo;
+  q.scale = scale;
+  q.amax = static_cast<float*>(workspace);
+  hipError_t e = swvr::quant_launch(q, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "quantisation launch");
   return SWVR_OK;
 }
 

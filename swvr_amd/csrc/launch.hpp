@@ -18,6 +18,7 @@ enum KernelKind {
   kKindPack,
   kKindBwdExpand,
   kKindLoss,
+  kKindQuant,
   kNumKinds
 };
 
@@ -141,6 +142,20 @@ struct MseParams {
   float* glse;          // [N] or null (with gO)
 };
 size_t mse_workspace_bytes(int N);
+
+// ---------------------------------------------------------------- e4m3 quantisation
+struct QuantParams {
+  const void* x;   // [R][ld], x_dtype (0 bf16, 1 f16, 2 f32)
+  int64_t ld;
+  int x_dtype;
+  int R, K, Kp;    // rows, columns, output columns (zero past K)
+  int per_row;     // scales per row ([R]) or one for the matrix ([1])
+  void* out;       // e4m3 bytes [R][ldo]
+  int64_t ldo;
+  float* scale;
+  float* amax;     // per-tensor: [R] row amaxes (workspace)
+};
+hipError_t quant_launch(const QuantParams& q, hipStream_t stream);
 hipError_t mse_launch(const MseParams& p, void* ws, hipStream_t stream);
 
 }  // namespace swvr

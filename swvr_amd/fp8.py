@@ -6,8 +6,8 @@ inference and evaluation, outside that policy and with its own tolerance:
 
 * W is quantised per vocabulary row, ``W[v] ~ w_scale[v] * W_e4m3[v]``, and h
   per tensor, ``h ~ h_scale * h_e4m3``, each scale = amax / 448 (the largest
-  finite e4m3 value), rounding to nearest even (torch's ``float8_e4m3fn``
-  cast);
+  finite e4m3 value), rounding to nearest even (bit-identical to torch's
+  ``float8_e4m3fn`` cast of ``x / scale``; ``swvr_quantize_e4m3``);
 * the scores ``S = logit_scale * h_scale * w_scale[v] * (h_e4m3 . W_e4m3[v]) + b``
   accumulate in fp32 on gfx950's k64 e4m3 matrix instruction, at twice the bf16
   rate; P is rounded to bf16 for ``P @ E`` as in the bf16 forward; O and LSE
@@ -25,27 +25,40 @@ from ._ops import _require_device
 
 E4M3 = torch.float8_e4m3fn
 E4M3_MAX = 448.0
-_TINY = 1e-30
 
 
-def _pad16(x):
-    K = x.shape[-1]
+def _quantize(x, per_row):
+    """``swvr_quantize_e4m3`` of a [R, K] matrix: (e4m3 [R, Kp], fp32 scales), Kp = K padded to 16."""
+    _require_device(x)
+    lib = _lib.load()
+    x = x.detach()
+    if x.dtype not in _lib.DTYPE_TAG:
+        x = x.to(torch.float32)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    R, K = x.shape
     Kp = (K + 15) // 16 * 16
-    return torch.nn.functional.pad(x, (0, Kp - K)) if Kp != K else x
+    out = torch.empty(R, Kp, dtype=E4M3, device=x.device)
+    scale = torch.empty(R if per_row else 1, dtype=torch.float32, device=x.device)
+    ws_bytes = lib.swvr_quantize_e4m3_workspace_size(R, int(per_row))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    ld = x.stride(0) if R > 1 else K
+    with torch.cuda.device(x.device):
+        rc = lib.swvr_quantize_e4m3(R, K, Kp, _lib.ptr(x), ld, _lib.DTYPE_TAG[x.dtype], int(per_row), _lib.ptr(out),
+                                    Kp, _lib.ptr(scale), _lib.ptr(ws), ws_bytes, _lib.stream_of(x.device))
+    _lib.check(rc)
+    return out, scale
 
 
 def quantize_rows(W):
-    """``(W_e4m3 [V, Kp], w_scale [V] fp32)`` with one scale per row (Kp: K padded to 16)."""
-    W32 = _pad16(W.detach().to(torch.float32))
-    scale = W32.abs().amax(dim=1).clamp_min(_TINY) / E4M3_MAX
-    return (W32 / scale[:, None]).to(E4M3).contiguous(), scale.contiguous()
+    """``(W_e4m3 [V, Kp], w_scale [V] fp32)`` with one scale per row, ``max(amax, 1e-30) / 448``
+    (Kp: K padded to 16 with zero bytes)."""
+    return _quantize(W, True)
 
 
 def quantize_tensor(h):
     """``(h_e4m3 [N, Kp], h_scale [1] fp32)`` with one scale for the whole matrix."""
-    h32 = _pad16(h.detach().to(torch.float32))
-    scale = (h32.abs().amax().clamp_min(_TINY) / E4M3_MAX).reshape(1)
-    return (h32 / scale).to(E4M3).contiguous(), scale
+    return _quantize(h, False)
 
 
 def dequantize(q, scale):

@@ -71,6 +71,37 @@ def test_fp8_masks_leading_dims_and_reuse_of_a_quantised_W():
     assert rel_err(O.reshape(N, D), Or) <= 1e-2 and rel_err(lse.reshape(N), lr) <= 1e-5
 
 
+def torch_quantize(x, per_row):
+    """The quantisation rule in torch ops: scale = max(amax, 1e-30) / 448, q = e4m3(x / scale)."""
+    x32 = x.to(torch.float32)
+    Kp = (x.shape[1] + 15) // 16 * 16
+    x32 = torch.nn.functional.pad(x32, (0, Kp - x.shape[1]))
+    if per_row:
+        scale = x32.abs().amax(dim=1).clamp_min(1e-30) / 448.0
+        return (x32 / scale[:, None]).to(fp8.E4M3), scale
+    scale = (x32.abs().amax().clamp_min(1e-30) / 448.0).reshape(1)
+    return (x32 / scale).to(fp8.E4M3), scale
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("R,K", [(1000, 2560), (37, 100), (5, 7), (1, 16)])
+def test_quantisation_is_bit_identical_to_the_torch_cast(dtype, R, K):
+    g = torch.Generator(device="cuda").manual_seed(R + K)
+    x = (torch.randn(R, K, device="cuda", generator=g) * torch.logspace(-3, 2, R, device="cuda")[:, None]).to(dtype)
+    x[0, :3] = 0.0
+    if R > 2:
+        x[2] = 0.0                                    # an all-zero row: tiny scale, zero bytes
+    for per_row in (True, False):
+        q, s = fp8._quantize(x, per_row)
+        qr, sr = torch_quantize(x, per_row)
+        assert torch.equal(s, sr), per_row
+        assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)), per_row
+    xs = x[:, : K // 2] if K >= 4 else x               # a strided view (leading dim > K)
+    q, s = fp8._quantize(xs, True)
+    qr, sr = torch_quantize(xs, True)
+    assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr)
+
+
 def test_fp8_is_forward_only_and_caps_D():
     h, W, E, b = make(64, 64, 500, 8)
     with pytest.raises(RuntimeError, match="forward only"):
