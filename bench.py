@@ -138,6 +138,37 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_mib": mib, "launches": 5}), flush=True)
 
 
+def fp8_forward(h, W, E, b, fwd_flops, iters):
+    """The opt-in e4m3 forward (swvr_amd.fp8) on the same inputs, reported beside the bf16
+    line (not part of it): W quantised once, as a server would keep it; each call quantises h.
+    TF/s count the same 2NV(K+D) as the bf16 forward."""
+    from swvr_amd import _lib, fp8
+    with torch.no_grad():
+        fp8.quantize_rows(W)  # first call: kernel load
+        q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        q0.record()
+        wq = fp8.quantize_rows(W)
+        q1.record()
+        fp8.softmax_readout_fp8(h, W, E, b, w_q=wq)
+        torch.cuda.synchronize()
+        _lib.kernel_timing(True)
+        _lib.kernel_timing(None)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(iters):
+            fp8.softmax_readout_fp8(h, W, E, b, w_q=wq)
+        s1.record()
+        torch.cuda.synchronize()
+        k = _lib.kernel_timing(None)
+        _lib.kernel_timing(False)
+    del wq
+    ms = s0.elapsed_time(s1) / iters
+    tile = k["fwd_tile_kernel"][0] / iters
+    return {"ms": round(ms, 3), "tflops": round(fwd_flops / (ms * 1e-3) / 1e12, 1),
+            "tile_kernel_ms": round(tile, 3), "tile_kernel_tflops": round(fwd_flops / (tile * 1e-3) / 1e12, 1),
+            "w_quantise_ms": round(q0.elapsed_time(q1), 3), "dtype": "e4m3 h and W, bf16 E and P"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -212,6 +243,7 @@ def main():
 
     fwd_flops, flops = algorithmic_flops(N, K, V, D)
     tflops = flops / (ms * 1e-3) / 1e12
+    fp8_fwd = fp8_forward(h, W, E, b, fwd_flops, fwd_iters) if D <= 128 else None
     # tokens with a non-zero weight: the others have zero cotangents, and the
     # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
     n_act = int((weight != 0).sum().item()) if weight is not None else N
@@ -247,6 +279,7 @@ def main():
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic(args.config, dom)},
+        "fp8_fwd": fp8_fwd,
         "published_reference_ms": {"A100": {3: 240, 2: 115, 4: 160}.get(args.config),
                                    "H200": {3: 98, 2: 48, 4: 62}.get(args.config)},
     }
