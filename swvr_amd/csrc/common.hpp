@@ -725,33 +725,89 @@ __device__ __forceinline__ void mfma_f8_k64(f32x16_t& c, i32x8_t a, i32x8_t b) {
 }
 
 // tile_reduce for e4m3 operands packed as if they were bf16 pairs: a staged
-// 64-byte row slice holds 64 k-values, and one k64 MFMA consumes it.  Each
+// 64-byte row slice holds 64 k-values, and one k64 MFMA consumes it.  Software-
+// pipelined like tile_reduce, with the slice as the step.  Each
 // lane's 32 operand bytes are the two 16-byte pieces the bf16 reduction reads
 // for its two k16 steps (bytes 16 hi .. 16 hi + 15 and 32 + 16 hi .. 32 + 16 hi
 // + 15 of the slice, hi = lane / 32).  A and B take the same bytes per lane, so
 // whatever order the instruction gives the k-values inside its 64, every
 // product pairs h[n, k] with W[v, k] of the same k.
-template <int L, int FM, int FN, class TA, class TB, class R, class F>
+// PIPE = false: one operand set, each slice read and then multiplied (fewer
+// registers).
+template <int L, bool PIPE, int FM, int FN, class TA, class TB, class R, class F>
 __device__ __forceinline__ void tile_reduce_f8(f32x16_t (&acc)[FM][FN], const TA&, const TB&, const char* smem,
                                                int sb, R& ring, int nk, int a_row0, int b_row0, F&& issue_next) {
   OpOffsets<typename TA::Layout, FM, 2> ao;
   ao.init(a_row0);
   OpOffsets<typename TB::Layout, FN, 2> bo;
   bo.init(b_row0);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt > 0) ring.template publish_next<L>();
-    const char* sA = smem + ring.slot * sb;
-    const char* sB = sA + TA::BYTES;
-    issue_next();
-    i32x8_t b[FN];
+  auto rd_a = [&](const char* s, int fm) { return cat16(ao.read(s, 0, fm), ao.read(s, 1, fm)); };
+  auto rd_b = [&](const char* s, int fn) { return cat16(bo.read(s + TA::BYTES, 0, fn), bo.read(s + TA::BYTES, 1, fn)); };
+  if constexpr (!PIPE) {
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt > 0) ring.template publish_next<L>();
+      const char* sA = smem + ring.slot * sb;
+      issue_next();
+      i32x8_t b[FN];
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) b[fn] = cat16(bo.read(sB, 0, fn), bo.read(sB, 1, fn));
+      for (int fn = 0; fn < FN; ++fn) b[fn] = rd_b(sA, fn);
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const i32x8_t a = cat16(ao.read(sA, 0, fm), ao.read(sA, 1, fm));
+      for (int fm = 0; fm < FM; ++fm) {
+        const i32x8_t a = rd_a(sA, fm);
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[fm][fn], a, b[fn]);
+        for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[fm][fn], a, b[fn]);
+      }
     }
+    return;
+  }
+  // one slice on operands x, with the next slice's operands read into y: the
+  // first row of MFMAs goes ahead of the wait + barrier that publishes the next
+  // stage, the rest run while y is read
+  auto step = [&](const i32x8_t (&xa)[FM], const i32x8_t (&xb)[FN], i32x8_t (&ya)[FM], i32x8_t (&yb)[FN]) {
+    issue_next();
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[0][fn], xa[0], xb[fn]);
+    __builtin_amdgcn_sched_barrier(0);
+    ring.template publish_next<L>();
+    __builtin_amdgcn_sched_barrier(0);
+    const char* nA = smem + ring.slot * sb;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) yb[fn] = rd_b(nA, fn);
+    ya[0] = rd_a(nA, 0);
+#pragma unroll
+    for (int fm = 1; fm < FM; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[fm][fn], xa[fm], xb[fn]);
+      ya[fm] = rd_a(nA, fm);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto last = [&](const i32x8_t (&xa)[FM], const i32x8_t (&xb)[FN]) {
+    issue_next();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) mfma_f8_k64(acc[fm][fn], xa[fm], xb[fn]);
+  };
+  // two register sets in turn, so no operand is copied between slices
+  i32x8_t pa[FM], pb[FN], qa[FM], qb[FN];
+  {
+    const char* sA = smem + ring.slot * sb;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) pb[fn] = rd_b(sA, fn);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) pa[fm] = rd_a(sA, fm);
+  }
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(pa, pb, qa, qb);
+    step(qa, qb, pa, pb);
+  }
+  if (kt + 1 < nk) {
+    step(pa, pb, qa, qb);
+    last(qa, qb);
+  } else {
+    last(pa, pb);
   }
 }
 

@@ -44,15 +44,19 @@ struct FwdTile {
 
 // The e4m3 forward (h and W in OCP e4m3, E and P in bf16): one k64 MFMA per
 // 64-byte slice takes 32 operand bytes per lane, twice the bf16 k16 step's, so
-// each wave owns 128 vocabulary rows x 32 tokens (the 128 x 64 wave of the
-// bf16 tile would not fit its accumulators and operands in 256 registers).
+// the 128 x 64 wave of the bf16 tile would not fit its accumulators and
+// operands in 256 registers.  D <= 64: waves of 64 x 64 (one operand read per
+// MFMA), a 4-deep ring of 24 KB slices and the software-pipelined reduction
+// (two operand sets).  D = 128 (wider E^T tile and accumulators): 128 x 32
+// waves, 3 slices, one operand set.
 static_assert(kFP8 == kFwdFP8, "one dtype code for the e4m3 forward");
 
 template <int DP>
 struct FwdTileF8 {
-  static constexpr int BV = 256, BM = 128, WV = 2, WT = 4;
+  static constexpr bool pipe = DP <= 64;
+  static constexpr int BV = 256, BM = 128, WV = pipe ? 4 : 2, WT = pipe ? 2 : 4;
   static constexpr int NT = 64 * WV * WT;
-  static constexpr int NS = 3;
+  static constexpr int NS = pipe ? 4 : 3;
 };
 
 template <class T, int DP, bool F8>
@@ -179,7 +183,7 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
     if constexpr (F8)
-      tile_reduce_f8<L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
+      tile_reduce_f8<L, FwdTileF8<DP>::pipe>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
     else
       tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
     if (nk < NS) {
@@ -426,9 +430,10 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   } else if (dtype == kFP8) {
     // K counts byte pairs: the e4m3 rows are packed as bf16 rows of K / 2 elements
     if (DP > 128) return false;
+    static_assert(FwdTileF8<128>::BV == FwdTileF8<64>::BV && FwdTileF8<128>::BM == FwdTileF8<64>::BM, "one tile");
     BV = FwdTileF8<64>::BV;
     BM = FwdTileF8<64>::BM;
-    WV = FwdTileF8<64>::WV;
+    WV = DP <= 64 ? FwdTileF8<64>::WV : FwdTileF8<128>::WV;
     tbytes = 2;
   } else {
     return false;
