@@ -157,12 +157,27 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
  * scores S = logit_scale * h_scale * w_scale[v] * (h_e4m3 . W_e4m3[v]) + bias
  * accumulate in fp32; P is rounded to bf16 for P.E as in the bf16 forward; E
  * is bf16 [V][lde]; O and lse are fp32.  K, ldh and ldw are multiples of 16
- * (bytes), h and W 16-byte aligned; D <= 128.  There is no e4m3 backward:
- * gradients come from swvr_bwd on bf16 operands. */
+ * (bytes), h and W 16-byte aligned; D <= 128.  Its backward, which
+ * recomputes the same scores, is swvr_bwd_fp8. */
 size_t swvr_fwd_fp8_workspace_size(int64_t N, int64_t K, int64_t V, int64_t D);
 int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const float* h_scale,
                  const void* W, int64_t ldw, const float* w_scale, const void* E, int64_t lde, const float* bias,
                  float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of the e4m3 forward (opt-in; no reference counterpart): swvr_bwd
+ * for bf16 h, W and E, with the scores recomputed from the e4m3 operands the
+ * forward used (hq [N][ldhq], Wq [V][ldwq], K8 bytes per row, and their
+ * scales), so P is the forward's.  The gradient products use the bf16 h and W:
+ * gh = s dS W, gW = s dS^T h, as swvr_bwd.  K8 >= K, K8, ldhq and ldwq
+ * multiples of 16; D <= 128. */
+size_t swvr_bwd_fp8_workspace_size(int64_t N, int64_t K, int64_t K8, int64_t V, int64_t D, int64_t chunk,
+                                   int need_gh);
+int swvr_bwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W, int64_t ldw,
+                 const void* E, int64_t lde, const float* bias, float logit_scale, const void* hq, int64_t K8,
+                 int64_t ldhq, const float* h_scale, const void* Wq, int64_t ldwq, const float* w_scale,
+                 const float* O, const float* lse, const float* gO, const float* glse, int64_t chunk, void* gh,
+                 int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype, float* gb, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* OCP e4m3 quantisation of h or W for swvr_fwd_fp8 (no reference
  * counterpart).  x is [R][ld] in x_dtype (SWVR_BF16, SWVR_F16, SWVR_F32);

@@ -40,6 +40,9 @@ SIGNATURES = {
     "swvr_fwd_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "swvr_fwd_fp8": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _f,
                           _p, _p, _p, _sz, _p]),
+    "swvr_bwd_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i]),
+    "swvr_bwd_fp8": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f, _p, _i64, _i64, _p, _p,
+                          _i64, _p, _p, _p, _p, _p, _i64, _p, _i, _p, _i, _p, _i, _p, _p, _sz, _p]),
     "swvr_quantize_e4m3_workspace_size": (_sz, [_i64, _i]),
     "swvr_quantize_e4m3": (_i, [_i64, _i64, _i64, _p, _i64, _i, _i, _p, _i64, _p, _p, _sz, _p]),
     "swvr_mse_loss_workspace_size": (_sz, [_i64]),

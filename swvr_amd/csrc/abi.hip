@@ -148,6 +148,67 @@ int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_
   return SWVR_OK;
 }
 
+int bwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
+                   int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
+                   float logit_scale, const float* O, const float* lse, const float* gO, const float* glse,
+                   int64_t chunk, void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype, float* gb,
+                   void* workspace, size_t workspace_bytes, void* stream, const void* hq = nullptr,
+                   int64_t K8 = 0, int64_t ldhq = 0, const float* h_scale = nullptr, const void* Wq = nullptr,
+                   int64_t ldwq = 0, const float* w_scale = nullptr) {
+  g_err[0] = 0;
+  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
+  if (rc != SWVR_OK) return rc;
+  if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
+  if (chunk <= 0) return fail(SWVR_EINVAL, "chunk must be positive, got %lld", (long long)chunk);
+  if (gh && !is_dtype(gh_dtype)) return fail(SWVR_EDTYPE, "unsupported gh dtype tag %d", gh_dtype);
+  if (gW && !is_dtype(gW_dtype)) return fail(SWVR_EDTYPE, "unsupported gW dtype tag %d", gW_dtype);
+  if (gE && !is_dtype(gE_dtype)) return fail(SWVR_EDTYPE, "unsupported gE dtype tag %d", gE_dtype);
+  if (gb && !bias) return fail(SWVR_EINVAL, "gb requested without a bias");
+  if (N > 0 && (!lse || !glse || (D > 0 && (!O || !gO)))) return fail(SWVR_EINVAL, "O, lse, gO and glse must be non-null");
+  BwdPlan plan;
+  if (!bwd_plan(dtype, N, K, V, D, chunk, gh != nullptr, &plan, w_dtype != dtype, hq ? K8 : 0))
+    return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (N > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
+    return fail(SWVR_EWORKSPACE, "backward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+  BwdParams p{};
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  p.O = O;
+  p.lse = lse;
+  p.gO = gO;
+  p.glse = glse;
+  p.gh = gh;
+  p.gh_dtype = gh_dtype;
+  p.gW = gW;
+  p.gW_dtype = gW_dtype;
+  p.gE = gE;
+  p.gE_dtype = gE_dtype;
+  p.gb = gb;
+  p.ws = static_cast<char*>(workspace);
+  p.h_f32 = h_dtype != dtype;
+  p.w_f32 = w_dtype != dtype;
+  p.hq = hq;
+  p.ldhq = ldhq;
+  p.Wq = Wq;
+  p.ldwq = ldwq;
+  p.h_scale = h_scale;
+  p.w_scale = w_scale;
+  p.K8 = (int)K8;
+  hipError_t e = bwd_launch(dtype, plan, p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "backward launch");
+  return SWVR_OK;
+}
+
 }  // namespace
 
 }  // namespace swvr
@@ -228,51 +289,36 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    float logit_scale, const float* O, const float* lse, const float* gO, const float* glse,
                    int64_t chunk, void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype, float* gb,
                    void* workspace, size_t workspace_bytes, void* stream) {
-  g_err[0] = 0;
-  int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
-  if (rc != SWVR_OK) return rc;
-  if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
-  if (chunk <= 0) return fail(SWVR_EINVAL, "chunk must be positive, got %lld", (long long)chunk);
-  if (gh && !is_dtype(gh_dtype)) return fail(SWVR_EDTYPE, "unsupported gh dtype tag %d", gh_dtype);
-  if (gW && !is_dtype(gW_dtype)) return fail(SWVR_EDTYPE, "unsupported gW dtype tag %d", gW_dtype);
-  if (gE && !is_dtype(gE_dtype)) return fail(SWVR_EDTYPE, "unsupported gE dtype tag %d", gE_dtype);
-  if (gb && !bias) return fail(SWVR_EINVAL, "gb requested without a bias");
-  if (N > 0 && (!lse || !glse || (D > 0 && (!O || !gO)))) return fail(SWVR_EINVAL, "O, lse, gO and glse must be non-null");
+  return bwd_common(dtype, h_dtype, w_dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, gO, glse,
+                    chunk, gh, gh_dtype, gW, gW_dtype, gE, gE_dtype, gb, workspace, workspace_bytes, stream);
+}
+
+size_t swvr_bwd_fp8_workspace_size(int64_t N, int64_t K, int64_t K8, int64_t V, int64_t D, int64_t chunk,
+                                   int need_gh) {
   BwdPlan plan;
-  if (!bwd_plan(dtype, N, K, V, D, chunk, gh != nullptr, &plan, w_dtype != dtype))
-    return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
-  if (N > 0 && (!workspace || workspace_bytes < plan.ws_bytes))
-    return fail(SWVR_EWORKSPACE, "backward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
-  BwdParams p;
-  p.h = h;
-  p.ldh = ldh;
-  p.W = W;
-  p.ldw = ldw;
-  p.E = E;
-  p.lde = lde;
-  p.bias = bias;
-  p.scale = logit_scale;
-  p.N = (int)N;
-  p.K = (int)K;
-  p.V = (int)V;
-  p.D = (int)D;
-  p.O = O;
-  p.lse = lse;
-  p.gO = gO;
-  p.glse = glse;
-  p.gh = gh;
-  p.gh_dtype = gh_dtype;
-  p.gW = gW;
-  p.gW_dtype = gW_dtype;
-  p.gE = gE;
-  p.gE_dtype = gE_dtype;
-  p.gb = gb;
-  p.ws = static_cast<char*>(workspace);
-  p.h_f32 = h_dtype != dtype;
-  p.w_f32 = w_dtype != dtype;
-  hipError_t e = bwd_launch(dtype, plan, p, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, "backward launch");
-  return SWVR_OK;
+  if (N < 0 || V < 0 || D < 0 || chunk <= 0 || K8 <= 0 ||
+      !bwd_plan(SWVR_BF16, N, K, V, D, chunk, need_gh != 0, &plan, false, K8))
+    return 0;
+  return plan.ws_bytes;
+}
+
+int swvr_bwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W, int64_t ldw,
+                 const void* E, int64_t lde, const float* bias, float logit_scale, const void* hq, int64_t K8,
+                 int64_t ldhq, const float* h_scale, const void* Wq, int64_t ldwq, const float* w_scale,
+                 const float* O, const float* lse, const float* gO, const float* glse, int64_t chunk, void* gh,
+                 int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype, float* gb, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  if (D > 128) return fail(SWVR_EDTYPE, "D=%lld exceeds the maximum 128 of the e4m3 scores", (long long)D);
+  if (K8 < K || K8 % 16 != 0 || ldhq < K8 || ldhq % 16 != 0 || ldwq < K8 || ldwq % 16 != 0)
+    return fail(SWVR_EINVAL, "K8=%lld (>= K), ldhq=%lld and ldwq=%lld (>= K8) must be multiples of 16",
+                (long long)K8, (long long)ldhq, (long long)ldwq);
+  if (K8 > ((int64_t)1 << 22)) return fail(SWVR_EINVAL, "K8=%lld too large", (long long)K8);
+  if (N > 0 && V > 0 && (!hq || !Wq || !h_scale || !w_scale || !aligned16(hq) || !aligned16(Wq)))
+    return fail(SWVR_EINVAL, "hq, Wq (16-byte aligned), h_scale and w_scale must be non-null");
+  return bwd_common(SWVR_BF16, SWVR_BF16, SWVR_BF16, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse,
+                    gO, glse, chunk, gh, gh_dtype, gW, gW_dtype, gE, gE_dtype, gb, workspace, workspace_bytes, stream,
+                    hq, K8, ldhq, h_scale, Wq, ldwq, w_scale);
 }
 
 int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh, const void* W,

@@ -12,6 +12,8 @@
 //     dW_c = s stage^T h   and   dh += s stage W_c                bwd_gemm_kernel
 //     dE_c, db_c = fixed-order sum of the partials                bwd_reduce_kernel
 // Every reduction has a fixed order, so gradients are bitwise reproducible.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -182,6 +184,7 @@ struct ScoresParams {
   int hS;               // reduction slices of both
   const void* Ep;       // packed E [V_pad][DP]
   const float* biasp;   // packed bias [V_pad]
+  const float* multp;   // e4m3 scores: logit_scale * h_scale * w_scale[v], [V_pad]; else null
   float scale;
   int N, K;
   const void* gOp;      // packed gO [N_pad][DP]
@@ -266,7 +269,9 @@ struct ScoresTile {
 // group (one partial per token-wave row).  Scores use the S layout (A = h
 // rows, B = W rows): a lane holds one vocabulary column and the registers
 // hold tokens, which is the B-operand layout P needs for dE^T = gO^T P.
-template <class T, int DP>
+// F8: h and W packed from e4m3 bytes (read as bf16 pairs); the k64 e4m3
+// reduction recomputes the scores the e4m3 forward computed.
+template <class T, int DP, bool F8 = false>
 __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(ScoresParams p) {
   typedef ScoresTile<T, DP> C;
   typedef typename Vec8<T>::type V8;
@@ -376,7 +381,10 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
     for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
       for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
-    tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    if constexpr (F8)
+      tile_reduce_f8<L, false>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    else
+      tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
     if (nk <= NS) {
       // short reduction: the side loads (gO / LSE / delta, and E / bias of
       // the first block) may still be in flight
@@ -390,6 +398,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
     for (int fv = 0; fv < FV; ++fv) {
       const int vl = wv * WVR + fv * 32 + (lane & 31);  // tile-local row of this lane
       const float bvv = vl < rows ? sBias[vl] : kNegInf;
+      const float mvv = F8 ? (vl < rows ? p.multp[vg0 + vl] : 0.f) : p.scale;
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
         // LDS bases recomputed per block (see opaque_zero)
@@ -416,7 +425,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * g4 + i;
-            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv) - lv[i]);
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], mvv, bvv) - lv[i]);
             const float ds = pv * (dp[r] - dv[i]);
             dbs += ds;
             sacc[ft][fv][r] = pv;
@@ -491,7 +500,7 @@ struct ScoresRingTile {
   static constexpr int BM = 256, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
 };
 
-template <class T, int DP>
+template <class T, int DP, bool F8 = false>
 __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   typedef ScoresRingTile<T, DP> C;
   typedef typename Vec8<T>::type V8;
@@ -527,12 +536,13 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   const int n_blocks = tb_end - tb_begin;
 
   f32x16_t deacc[DB][FV];
-  float dbacc[FV], bvv[FV];
+  float dbacc[FV], bvv[FV], mvv[FV];
 #pragma unroll
   for (int fv = 0; fv < FV; ++fv) {
     dbacc[fv] = 0.f;
     const int vl = wv * WVR + fv * 32 + (lane & 31);
     bvv[fv] = vl < rows ? p.biasp[vg0 + vl] : kNegInf;
+    mvv[fv] = F8 ? (vl < rows ? p.multp[vg0 + vl] : 0.f) : p.scale;
 #pragma unroll
     for (int db = 0; db < DB; ++db) deacc[db][fv] = zero16();
   }
@@ -616,7 +626,10 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
     for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
       for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
-    tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    if constexpr (F8)
+      tile_reduce_f8<L, false>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    else
+      tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
     ring.template publish_next<L>();  // E
     issue_next();                     // the next block's slice 0 into the last slice's slot
     ring.template publish_next<L>();  // gO
@@ -659,7 +672,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * g4 + i;
-            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv[fv]) - lv[i]);
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], F8 ? mvv[fv] : p.scale, bvv[fv]) - lv[i]);
             const float ds = pv * (dp[r] - dv[i]);
             dbs += ds;
             sacc[ft][fv][r] = pv;
@@ -1085,19 +1098,19 @@ struct ScoresRing {
   static constexpr bool value = sizeof(T) == 2 && DP <= 64;
 };
 
-template <class T, int DP>
+template <class T, int DP, bool F8 = false>
 hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   if constexpr (ScoresRing<T, DP>::value) {
     typedef ScoresRingTile<T, DP> C;
     if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
-    bwd_scores_ring_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    bwd_scores_ring_kernel<T, DP, F8><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
     timing_end(kKindBwdScores, stream);
   } else {
     typedef ScoresTile<T, DP> C;
     if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
-    bwd_scores_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    bwd_scores_kernel<T, DP, F8><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
     timing_end(kKindBwdScores, stream);
   }
   return hipGetLastError();
@@ -1105,6 +1118,17 @@ hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_
 
 template <class T>
 hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    if (sp.multp) {  // e4m3 scores (bf16 compute dtype only)
+      switch (plan.DP) {
+        case 32: return launch_scores<T, 32, true>(plan, sp, stream);
+        case 64: return launch_scores<T, 64, true>(plan, sp, stream);
+        case 128: return launch_scores<T, 128, true>(plan, sp, stream);
+        default: return hipErrorInvalidValue;
+      }
+    }
+  }
+  if (sp.multp) return hipErrorInvalidValue;
   switch (plan.DP) {
     case 32: return launch_scores<T, 32>(plan, sp, stream);
     case 64: return launch_scores<T, 64>(plan, sp, stream);
@@ -1152,6 +1176,10 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   T* Wc = (sizeof(T) == 2 && p.w_f32) ? reinterpret_cast<T*>(ws + plan.off_Wc) : nullptr;
   const void* Wr = Wc ? static_cast<const void*>(Wc) : p.W;
   const int64_t ldwr = Wc ? p.K : p.ldw;
+  // e4m3 scores: e4m3 h over positions (bytes, read as K8 / 2 pairs) and the per-row multipliers
+  const bool f8 = p.hq != nullptr;
+  T* hqc = reinterpret_cast<T*>(ws + plan.off_hqc);
+  float* multp = f8 ? reinterpret_cast<float*>(ws + plan.off_mult) : nullptr;
 
   {
     // delta, the active tokens, and the token-side operands over positions
@@ -1167,7 +1195,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     const int64_t nv = (int64_t)plan.V_pad * plan.DP;
     timing_begin(kKindPack, stream);
     pack_vocab_kernel<T><<<(int)((nv + 255) / 256), 256, 0, stream>>>(
-        static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp);
+        static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, Ep, biasp, p.h_scale, p.w_scale,
+        p.scale, multp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (p.K > 0) {
       const int64_t nh = plan.N_pad * (p.K / (16 / (int)sizeof(T)));
@@ -1180,11 +1209,25 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
                                                               (int)plan.N_pad, p.K, hc);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
-      return e;
-    // fp32 W: the packing also writes the row-major copy the dh product reads
-    if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream, Wc)) != hipSuccess)
-      return e;
+    if (f8) {
+      // the scores kernel reads the e4m3 operands; the gradient GEMMs keep h over positions and W
+      const int k2 = p.K8 / 2;
+      const int64_t nq = plan.N_pad * (k2 / (16 / (int)sizeof(T)));
+      bwd_gather_rows_kernel<T, T><<<(unsigned)((nq + 255) / 256), 256, 0, stream>>>(
+          static_cast<const T*>(p.hq), p.ldhq / 2, idx, n_act, (int)plan.N_pad, k2, hqc);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if ((e = launch_pack_rows<T>(hqc, k2, (int)plan.N_pad, k2, plan.hS8, plan.N_pad, hp, stream)) != hipSuccess)
+        return e;
+      if ((e = pack_src<T>(p.Wq, false, p.ldwq / 2, p.V, k2, plan.hS8, plan.V_pad, Wp, stream, nullptr)) !=
+          hipSuccess)
+        return e;
+    } else {
+      if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
+        return e;
+      // fp32 W: the packing also writes the row-major copy the dh product reads
+      if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream, Wc)) != hipSuccess)
+        return e;
+    }
     timing_end(kKindPack, stream);
   }
 
@@ -1195,12 +1238,13 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     ScoresParams sp;
     sp.hp = hp;
     sp.Wp = Wp;
-    sp.hS = plan.hS;
+    sp.hS = f8 ? plan.hS8 : plan.hS;
     sp.Ep = Ep;
     sp.biasp = biasp;
+    sp.multp = multp;
     sp.scale = p.scale;
     sp.N = p.N;
-    sp.K = p.K;
+    sp.K = f8 ? p.K8 / 2 : p.K;
     sp.gOp = gOp;
     sp.gOt = gOt;
     sp.lsed = lsed;
@@ -1302,7 +1346,8 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 }  // namespace
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan,
-              bool w_f32) {
+              bool w_f32, int64_t K8) {
+  if (K8 > 0 && (dtype != kBF16 || D > 128 || K8 % 16 != 0)) return false;
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
   int BM, BV, GM, GN, WT, wgs;
@@ -1361,10 +1406,12 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->V_pad * 4);
   const int bk = dtype == kF32 ? SliceK<float>::value : SliceK<bf16_t>::value;
   plan->hS = packed_slices(K, bk);
+  plan->hS8 = K8 > 0 ? packed_slices(K8 / 2, bk) : 0;
+  const int hs_max = plan->hS > plan->hS8 ? plan->hS : plan->hS8;
   plan->off_hp = off;
-  off += align256((size_t)plan->N_pad * plan->hS * bk * tb);
+  off += align256((size_t)plan->N_pad * hs_max * bk * tb);
   plan->off_Wp = off;
-  off += align256((size_t)plan->V_pad * plan->hS * bk * tb);
+  off += align256((size_t)plan->V_pad * hs_max * bk * tb);
   plan->off_flag = off;
   off += align256((size_t)plan->N_pad * 4);
   plan->off_idx = off;
@@ -1379,6 +1426,10 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->N_pad * K * tb);
   plan->off_Wc = off;
   if (w_f32 && tb == 2) off += align256((size_t)V * K * tb);
+  plan->off_hqc = off;  // e4m3 h over positions, K8 bytes per row
+  if (K8 > 0) off += align256((size_t)plan->N_pad * K8);
+  plan->off_mult = off;
+  if (K8 > 0) off += align256((size_t)plan->V_pad * 4);
   plan->ws_bytes = off;
   return true;
 }

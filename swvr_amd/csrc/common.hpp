@@ -451,13 +451,18 @@ __device__ __forceinline__ typename Vec8<T>::type read_op(const RTile<T, R, BK, 
 template <class T>
 __global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E, int64_t lde,
                                                          const float* __restrict__ bias, int V, int D, int V_pad,
-                                                         int DP, T* __restrict__ Ep, float* __restrict__ biasp) {
+                                                         int DP, T* __restrict__ Ep, float* __restrict__ biasp,
+                                                         const float* __restrict__ h_scale = nullptr,
+                                                         const float* __restrict__ w_scale = nullptr,
+                                                         float logit_scale = 0.f, float* __restrict__ multp = nullptr) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e < (int64_t)V_pad * DP) {
     const int v = (int)(e / DP), d = (int)(e % DP);
     Ep[e] = (v < V && d < D) ? E[(int64_t)v * lde + d] : (T)0.f;
   }
   if (e < V_pad) biasp[e] = e < V ? (bias ? bias[e] : 0.f) : kNegInf;
+  // e4m3 scores: the factor that turns row v's e4m3 dot product into a score
+  if (multp && e < V_pad) multp[e] = e < V ? logit_scale * h_scale[0] * w_scale[e] : 0.f;
 }
 
 // Per-lane byte offsets, within one staged slice, of the operands of F

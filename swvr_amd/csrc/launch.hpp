@@ -90,12 +90,15 @@ struct BwdPlan {
   int hS;                // reduction slices of the packed h and W
   size_t off_stage, off_pe, off_pb, off_dh, off_gO, off_gOt, off_lsed, off_Ep, off_bias, off_hp, off_Wp;
   size_t off_flag, off_idx, off_inv, off_nact, off_delta, off_hc, off_Wc, ws_bytes;
+  int hS8;               // e4m3 scores: reduction slices of the packed e4m3 h and W (K8 / 2 pairs)
+  size_t off_hqc, off_mult;
 };
 
 // w_f32: W is stored in fp32 and needs a row-major copy in the compute dtype
 // (the dh product reads W rows directly).
+// K8 > 0: the scores are recomputed from e4m3 h and W of K8 bytes per row.
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh,
-              BwdPlan* plan, bool w_f32 = false);
+              BwdPlan* plan, bool w_f32 = false, int64_t K8 = 0);
 
 struct BwdParams {
   const void* h;
@@ -120,6 +123,15 @@ struct BwdParams {
   float* gb;
   char* ws;
   int h_f32, w_f32;    // h / W stored in fp32 (rounded to the compute dtype as they are read)
+  // e4m3 scores (null hq: the compute dtype's): h and W as e4m3 bytes, K8 per
+  // row, leading dims in bytes, with the forward's dequantisation scales
+  const void* hq;
+  int64_t ldhq;
+  const void* Wq;
+  int64_t ldwq;
+  const float* h_scale;
+  const float* w_scale;
+  int K8;
 };
 
 hipError_t bwd_launch(int dtype, const BwdPlan& plan, const BwdParams& p, hipStream_t stream);

@@ -16,12 +16,14 @@ inference and evaluation, outside that policy and with its own tolerance:
 Given the quantised operands, the result matches the fp64 readout of the
 dequantised h and W to the bf16 forward's tolerance; against the unquantised
 inputs the e4m3 rounding of h and W adds its own error (a few per cent of the
-scores' spread).  There is no fp8 backward: train with ``softmax_readout``.
+scores' spread).  The backward (``swvr_bwd_fp8``) recomputes the same e4m3 scores,
+so P is the forward's, and forms gh = s dS W and gW = s dS^T h from the bf16
+h and W (the quantisation passes gradients through as the identity).
 """
 import torch
 
 from . import _lib
-from ._ops import _require_device
+from ._ops import _grad_buffer, _kpad, _lead_stride, _matrix, _require_device
 
 E4M3 = torch.float8_e4m3fn
 E4M3_MAX = 448.0
@@ -66,42 +68,123 @@ def dequantize(q, scale):
     return q.to(torch.float32) * (scale[:, None] if scale.numel() > 1 else scale)
 
 
-def softmax_readout_fp8(h, W, E, bias=None, *, logit_scale=1.0, w_q=None):
+def _fwd(hq, hs, Wq, ws, E, bias, logit_scale):
+    lib = _lib.load()
+    N, Kq = hq.shape
+    V, D = E.shape
+    Eb = E.detach().to(torch.bfloat16)
+    Eb = Eb if Eb.stride(-1) == 1 else Eb.contiguous()
+    b = bias.detach().to(torch.float32).contiguous() if bias is not None else None
+    O = torch.empty(N, D, dtype=torch.float32, device=hq.device)
+    lse = torch.empty(N, dtype=torch.float32, device=hq.device)
+    ws_bytes = lib.swvr_fwd_fp8_workspace_size(N, Kq, V, D)
+    if ws_bytes == 0 and N > 0:
+        raise NotImplementedError(f"swvr_amd: no e4m3 forward for D={D} (at most 128)")
+    work = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=hq.device)
+    lde = Eb.stride(0) if V > 1 else D
+    with torch.cuda.device(hq.device):
+        rc = lib.swvr_fwd_fp8(N, Kq, V, D, _lib.ptr(hq), Kq, _lib.ptr(hs), _lib.ptr(Wq), Kq, _lib.ptr(ws),
+                              _lib.ptr(Eb), lde, _lib.ptr(b), float(logit_scale), _lib.ptr(O), _lib.ptr(lse),
+                              _lib.ptr(work), ws_bytes, _lib.stream_of(hq.device))
+    _lib.check(rc)
+    return O, lse
+
+
+def _bwd(gO, glse, h, W, E, bias, O, lse, hq, hs, Wq, ws, logit_scale, chunk, needs):
+    """``swvr_bwd_fp8``: the scores recomputed from the forward's e4m3 operands, the gradient
+    products on bf16 h and W (swvr/chunked.py:108-151 otherwise)."""
+    lib = _lib.load()
+    N, K = h.shape
+    V, D = E.shape
+    Kp = _kpad(K)
+    hb = _matrix(h.detach(), torch.bfloat16, Kp)
+    Wb = _matrix(W.detach(), torch.bfloat16, Kp)
+    Eb = E.detach().to(torch.bfloat16)
+    Eb = Eb if Eb.stride(-1) == 1 else Eb.contiguous()
+    b = bias.detach().to(torch.float32).contiguous() if bias is not None else None
+    need_h, need_W, need_E, need_b = needs
+    dev = h.device
+    gh = _grad_buffer((N, Kp), h.dtype, dev) if need_h else None
+    gW = _grad_buffer((V, Kp), W.dtype, dev) if need_W else None
+    gE = _grad_buffer((V, D), E.dtype, dev) if need_E else None
+    gb = torch.empty(V, dtype=torch.float32, device=dev) if need_b else None
+    gO32 = gO.to(torch.float32).contiguous()
+    glse32 = glse.to(torch.float32).contiguous()
+    Kq = hq.shape[1]
+    ws_bytes = lib.swvr_bwd_fp8_workspace_size(N, Kp, Kq, V, D, int(chunk), int(need_h))
+    work = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def tag_of(t):
+        return _lib.DTYPE_TAG[t.dtype] if t is not None else 0
+
+    lde = Eb.stride(0) if V > 1 else D
+    with torch.cuda.device(dev):
+        rc = lib.swvr_bwd_fp8(N, Kp, V, D, _lib.ptr(hb), _lead_stride(hb), _lib.ptr(Wb), _lead_stride(Wb),
+                              _lib.ptr(Eb), lde, _lib.ptr(b), float(logit_scale), _lib.ptr(hq), Kq, Kq,
+                              _lib.ptr(hs), _lib.ptr(Wq), Kq, _lib.ptr(ws), _lib.ptr(O), _lib.ptr(lse),
+                              _lib.ptr(gO32), _lib.ptr(glse32), int(chunk), _lib.ptr(gh), tag_of(gh), _lib.ptr(gW),
+                              tag_of(gW), _lib.ptr(gE), tag_of(gE), _lib.ptr(gb), _lib.ptr(work), ws_bytes,
+                              _lib.stream_of(dev))
+    _lib.check(rc)
+    if gh is not None:
+        gh = gh[:, :K] if Kp != K else gh
+        gh = gh.to(h.dtype) if gh.dtype != h.dtype else gh
+    if gW is not None:
+        gW = gW[:, :K].contiguous() if Kp != K else gW
+        gW = gW.to(W.dtype) if gW.dtype != W.dtype else gW
+    if gE is not None and gE.dtype != E.dtype:
+        gE = gE.to(E.dtype)
+    if gb is not None and gb.dtype != bias.dtype:
+        gb = gb.to(bias.dtype)
+    return gh, gW, gE, gb
+
+
+class _Fp8Readout(torch.autograd.Function):
+    """e4m3 forward; the backward recomputes the same e4m3 scores (so P is the forward's) and
+    takes the gradient products on bf16 h and W, treating the quantisation as the identity."""
+
+    @staticmethod
+    def forward(ctx, h2, W, E, bias, logit_scale, chunk, hq, hs, Wq, ws):
+        O, lse = _fwd(hq, hs, Wq, ws, E, bias, logit_scale)
+        ctx.save_for_backward(h2, W, E, bias, O, lse, hq, hs, Wq, ws)
+        ctx.args = (logit_scale, chunk)
+        return O, lse
+
+    @staticmethod
+    def backward(ctx, gO, glse):
+        h2, W, E, bias, O, lse, hq, hs, Wq, ws = ctx.saved_tensors
+        needs = [bool(n) for n in ctx.needs_input_grad[:4]]
+        needs[3] = needs[3] and bias is not None
+        gO = gO if gO is not None else torch.zeros_like(O)
+        glse = glse if glse is not None else torch.zeros_like(lse)
+        grads = _bwd(gO, glse, h2, W, E, bias, O, lse, hq, hs, Wq, ws, *ctx.args, needs)
+        return (*[g if n else None for g, n in zip(grads, needs)], None, None, None, None, None, None)
+
+
+def softmax_readout_fp8(h, W, E, bias=None, *, logit_scale=1.0, w_q=None, chunk_size=None):
     """``(O, LSE)`` of ``softmax(logit_scale * h @ W.T + bias) @ E`` with h and W in e4m3.
 
     Shapes as ``softmax_readout``: h ``[..., K]``, W ``[V, K]``, E ``[V, D]`` (D <= 128),
     bias ``[V]``.  ``w_q`` = ``quantize_rows(W)`` reuses a quantised W across calls (W is
-    then only used for its shape).  Forward only: raises if autograd would need gradients.
+    then only used for its shape, and for the gradient products).  Differentiable: the
+    backward recomputes the same e4m3 scores and stages ``chunk_size`` (default 8192)
+    vocabulary rows of dS at a time; gh, gW, gE and gb come out in the parameters' dtypes.
     """
-    from .api import _check
+    from .api import _check, default_chunk_size
     _check(h, W, E, bias)
     _require_device(h)
-    if torch.is_grad_enabled() and any(
-            t is not None and t.requires_grad for t in (h, W, E, bias)):
-        raise RuntimeError("softmax_readout_fp8 is forward only; use softmax_readout to train")
-    lib = _lib.load()
     lead = h.shape[:-1]
     h2 = h.reshape(-1, h.shape[-1])
-    N = h2.shape[0]
     V, D = E.shape
     hq, hs = quantize_tensor(h2)
     Wq, ws = w_q if w_q is not None else quantize_rows(W)
     if Wq.shape != (V, hq.shape[1]) or Wq.dtype != E4M3 or ws.shape != (V,):
         raise ValueError(f"w_q must be quantize_rows(W) of a [{V}, {W.shape[1]}] W")
-    Kp = hq.shape[1]
-    Eb = E.to(torch.bfloat16)
-    Eb = Eb if Eb.stride(-1) == 1 else Eb.contiguous()
-    b = bias.to(torch.float32).contiguous() if bias is not None else None
-    O = torch.empty(N, D, dtype=torch.float32, device=h.device)
-    lse = torch.empty(N, dtype=torch.float32, device=h.device)
-    ws_bytes = lib.swvr_fwd_fp8_workspace_size(N, Kp, V, D)
-    if ws_bytes == 0 and N > 0:
-        raise NotImplementedError(f"swvr_amd: no e4m3 forward for D={D} (at most 128)")
-    work = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
-    lde = Eb.stride(0) if V > 1 else D
-    with torch.cuda.device(h.device):
-        rc = lib.swvr_fwd_fp8(N, Kp, V, D, _lib.ptr(hq), Kp, _lib.ptr(hs), _lib.ptr(Wq), Kp, _lib.ptr(ws),
-                              _lib.ptr(Eb), lde, _lib.ptr(b), float(logit_scale), _lib.ptr(O), _lib.ptr(lse),
-                              _lib.ptr(work), ws_bytes, _lib.stream_of(h.device))
-    _lib.check(rc)
+    chunk = int(chunk_size) if chunk_size else default_chunk_size()
+    if chunk <= 0:
+        raise ValueError(f"chunk_size must be positive, got {chunk}")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (h, W, E, bias)):
+        O, lse = _Fp8Readout.apply(h2, W, E, bias, float(logit_scale), chunk, hq, hs, Wq, ws)
+    else:
+        O, lse = _fwd(hq, hs, Wq, ws, E, bias, logit_scale)
     return O.view(*lead, D), lse.view(lead)

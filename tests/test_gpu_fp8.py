@@ -10,7 +10,7 @@ import torch
 
 from oracle import reference as ref
 from swvr_amd import fp8
-from tests.gpu_util import rel_err
+from tests.gpu_util import cosine, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -102,10 +102,53 @@ def test_quantisation_is_bit_identical_to_the_torch_cast(dtype, R, K):
     assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr)
 
 
-def test_fp8_is_forward_only_and_caps_D():
-    h, W, E, b = make(64, 64, 500, 8)
-    with pytest.raises(RuntimeError, match="forward only"):
-        fp8.softmax_readout_fp8(h.requires_grad_(True), W, E, b)
+def mixed_grads(h, W, E, b, gO, glse, logit_scale, quantised=True):
+    """fp64 gradients of the e4m3 readout: scores from the dequantised h and W, the gradient
+    products on h and W as given (the quantisation passes gradients as the identity).
+    quantised=False: the scores from h and W themselves (the bf16 readout's gradients)."""
+    hq, hs = fp8.quantize_tensor(h)
+    Wq, ws = fp8.quantize_rows(W)
+    d = lambda t: t.detach().double().cpu()
+    hd, Wd = d(fp8.dequantize(hq, hs))[:, : h.shape[1]], d(fp8.dequantize(Wq, ws))[:, : W.shape[1]]
+    if not quantised:
+        hd, Wd = d(h), d(W)
+    S = logit_scale * hd @ Wd.T + (d(b) if b is not None else 0.0)
+    P = torch.softmax(S, dim=-1)
+    O = P @ d(E)
+    gO64, glse64 = d(gO), d(glse)
+    delta = (O * gO64).sum(-1) - glse64
+    dS = P * (gO64 @ d(E).T - delta[:, None])
+    return (logit_scale * dS @ d(W), logit_scale * dS.T @ d(h), P.T @ gO64, dS.sum(0))
+
+
+@pytest.mark.parametrize("N,K,V,D,chunk,bias", [(300, 512, 3000, 64, 1024, True), (517, 256, 4099, 5, 700, True),
+                                               (256, 80, 2000, 128, 1024, False), (64, 16, 1000, 32, 512, True)])
+def test_fp8_backward_matches_fp64_with_the_forwards_scores(N, K, V, D, chunk, bias):
+    g = torch.Generator(device="cuda").manual_seed(5)
+    h = torch.randn(N, K, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    W = (torch.randn(V, K, device="cuda", generator=g) / K ** 0.5).to(torch.bfloat16).requires_grad_(True)
+    E = torch.randn(V, D, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    b = (0.5 * torch.randn(V, device="cuda", generator=g)).requires_grad_(True) if bias else None
+    gO = torch.randn(N, D, device="cuda", generator=g)
+    glse = 0.1 * torch.randn(N, device="cuda", generator=g)
+    gO[::7] = 0.0
+    glse[::7] = 0.0  # zero cotangents: tokens the backward skips
+    xs = [x for x in (h, W, E, b) if x is not None]
+    O, lse = fp8.softmax_readout_fp8(h, W, E, b, logit_scale=0.8, chunk_size=chunk)
+    got = torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), xs)
+    want = mixed_grads(h, W, E, b, gO, glse, 0.8)
+    for name, a, r in zip(["gh", "gW", "gE", "gb"], got, want):
+        err, cos = rel_err(a, r), cosine(a, r)
+        print(N, K, V, D, name, f"rel {err:.1e} cos {cos:.6f}")
+        assert a.dtype == xs[["gh", "gW", "gE", "gb"].index(name)].dtype
+        assert err <= 2e-2 and cos >= 0.999, (name, err, cos)
+    assert torch.count_nonzero(got[0][::7]) == 0  # inactive tokens get zero rows
+    # the backward used the e4m3 scores: the gradients of bf16 scores are much farther away
+    other = mixed_grads(h, W, E, b, gO, glse, 0.8, quantised=False)
+    assert rel_err(got[1], other[1]) > 3 * rel_err(got[1], want[1])
+
+
+def test_fp8_caps_D():
     h, W, E, b = make(64, 64, 500, 200)
     with pytest.raises(NotImplementedError):
         fp8.softmax_readout_fp8(h, W, E, b)
