@@ -67,6 +67,12 @@ def softmax_readout_mse(h, W, E, target, bias=None, *, weight=None, reduction="m
     ``"none"`` are also accepted.
     """
     O, lse = softmax_readout(h, W, E, bias, logit_scale=logit_scale, chunk_size=chunk_size)
+    return _mse_loss(O, lse, target, weight, reduction, z_loss_weight)
+
+
+def _mse_loss(O, lse, target, weight, reduction, z_loss_weight):
+    """The loss of swvr/api.py:53-66 over the readout's O and lse: the library's loss kernels
+    where they apply, else the composite formula."""
     if _fusable_loss(O, lse, target, weight, reduction):
         D = O.shape[-1]
         out = mse_loss_op(O.reshape(-1, D), lse.reshape(-1), target.reshape(-1, D),

@@ -188,3 +188,12 @@ def softmax_readout_fp8(h, W, E, bias=None, *, logit_scale=1.0, w_q=None, chunk_
     else:
         O, lse = _fwd(hq, hs, Wq, ws, E, bias, logit_scale)
     return O.view(*lead, D), lse.view(lead)
+
+
+def softmax_readout_mse_fp8(h, W, E, target, bias=None, *, weight=None, reduction="mean", z_loss_weight=0.0,
+                            logit_scale=1.0, chunk_size=None, w_q=None):
+    """``softmax_readout_mse`` over the e4m3 readout: the same loss (swvr/api.py:53-66) on the
+    O and LSE of ``softmax_readout_fp8``."""
+    from .api import _mse_loss
+    O, lse = softmax_readout_fp8(h, W, E, bias, logit_scale=logit_scale, w_q=w_q, chunk_size=chunk_size)
+    return _mse_loss(O, lse, target, weight, reduction, z_loss_weight)
