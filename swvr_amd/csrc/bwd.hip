@@ -519,8 +519,11 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   constexpr int FT = WTR / 32, FV = WVR / 32;
   constexpr int DB = DP / 32, DK = DP / 16;
 
-  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4];
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4 + (F8 ? BV * 8 : 0)];
   float* const sLD = reinterpret_cast<float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
+  // F8: (bias, score factor) of the tile's rows, read in the epilogue (two fewer registers per
+  // row block than holding both); the bf16 kernel holds the bias in registers
+  float2* const sBM = reinterpret_cast<float2*>(smem + NS * SB + 2 * 2 * BM * 4);
 
   const int lane = lane_id(), w = wave_id();
   const int wt = w / C::WV, wv = w % C::WV;
@@ -535,14 +538,17 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   const int tb_end = (int)((int64_t)(g + 1) * n_tb_act / p.G);
   const int n_blocks = tb_end - tb_begin;
 
+  // visible to every wave after the first stage's barrier, before any epilogue
+  if constexpr (F8)
+    for (int i = threadIdx.x; i < BV; i += NT)
+      sBM[i] = make_float2(i < rows ? p.biasp[vg0 + i] : kNegInf, i < rows ? p.multp[vg0 + i] : 0.f);
   f32x16_t deacc[DB][FV];
-  float dbacc[FV], bvv[FV], mvv[FV];
+  float dbacc[FV], bvv[FV];
 #pragma unroll
   for (int fv = 0; fv < FV; ++fv) {
     dbacc[fv] = 0.f;
     const int vl = wv * WVR + fv * 32 + (lane & 31);
-    bvv[fv] = vl < rows ? p.biasp[vg0 + vl] : kNegInf;
-    mvv[fv] = F8 ? (vl < rows ? p.multp[vg0 + vl] : 0.f) : p.scale;
+    if constexpr (!F8) bvv[fv] = vl < rows ? p.biasp[vg0 + vl] : kNegInf;
 #pragma unroll
     for (int db = 0; db < DB; ++db) deacc[db][fv] = zero16();
   }
@@ -662,6 +668,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
         for (int kd = 0; kd < DK; ++kd)
           mfma_k16(dp, read_op(tgl, sGe, tr0 + lr, kd, ln), read_op(tel, sEe, vl, kd, ln));
         float dbs = 0.f;
+        const float2 bm = F8 ? sBM[vl] : make_float2(bvv[fv], p.scale);  // this lane's row: bias, score factor
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
@@ -672,7 +679,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * g4 + i;
-            const float pv = fast_exp(fmaf(sacc[ft][fv][r], F8 ? mvv[fv] : p.scale, bvv[fv]) - lv[i]);
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], bm.y, bm.x) - lv[i]);
             const float ds = pv * (dp[r] - dv[i]);
             dbs += ds;
             sacc[ft][fv][r] = pv;
