@@ -459,13 +459,13 @@ int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const 
   if (reduction < SWVR_REDUCE_NONE || reduction > SWVR_REDUCE_MEAN)
     return fail(SWVR_EINVAL, "unknown reduction %d", reduction);
   if (ldt < D) return fail(SWVR_EINVAL, "ldt=%lld must be >= D", (long long)ldt);
+  if (reduction == SWVR_REDUCE_NONE && N == 0) return SWVR_OK;  // nothing to write
   if (!out) return fail(SWVR_EINVAL, "out must be non-null");
   if ((gO == nullptr) != (glse == nullptr)) return fail(SWVR_EINVAL, "gO and glse must both be given or both NULL");
   if (N > 0 && (!O || !lse || !target)) return fail(SWVR_EINVAL, "O, lse and target must be non-null");
   const size_t need = reduction == SWVR_REDUCE_NONE ? 0 : swvr::mse_workspace_bytes((int)N);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(SWVR_EWORKSPACE, "loss workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-  if (reduction == SWVR_REDUCE_NONE && N == 0) return SWVR_OK;
   swvr::MseParams p{};
   p.O = O;
   p.lse = lse;

@@ -152,3 +152,22 @@ def test_fp8_caps_D():
     h, W, E, b = make(64, 64, 500, 200)
     with pytest.raises(NotImplementedError):
         fp8.softmax_readout_fp8(h, W, E, b)
+
+
+def test_fp8_edge_sizes_no_tokens_and_one_vocabulary_row():
+    # no tokens: empty outputs; the backward gives zero vocabulary gradients (as swvr_bwd)
+    h, W, E, b = make(0, 64, 300, 16)
+    xs = [x.requires_grad_(True) for x in (h, W, E, b)]
+    O, lse = fp8.softmax_readout_fp8(*xs)
+    assert O.shape == (0, 16) and lse.shape == (0,)
+    gW, gE, gb = torch.autograd.grad(O.sum() + lse.sum(), xs[1:], allow_unused=True)
+    for g in (gW, gE, gb):
+        assert g is None or torch.count_nonzero(g) == 0
+    # one vocabulary row: softmax is 1, O = E[0], lse = the score itself
+    h, W, E, b = make(40, 32, 1, 8)
+    O, lse = fp8.softmax_readout_fp8(h, W, E, b)
+    assert torch.allclose(O, E.float().expand(40, 8), rtol=0, atol=0)
+    hq, hs = fp8.quantize_tensor(h)
+    Wq, ws = fp8.quantize_rows(W)
+    S = (fp8.dequantize(hq, hs) @ fp8.dequantize(Wq, ws).T).squeeze(1) + b
+    assert rel_err(lse, S) < 1e-5

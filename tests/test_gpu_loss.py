@@ -132,3 +132,13 @@ def test_leading_dims_and_the_composite_cases():
     wb = weight[:60]
     loss = swvr.softmax_readout_mse(h3, xs[1], xs[2], t3, xs[3], weight=wb)
     assert rel_err(loss, formula(O, lse, t3, wb, 0.0, "mean")) < 1e-6
+
+
+def test_loss_over_no_tokens_follows_the_reference():
+    O = torch.empty(0, 8, device="cuda")
+    lse = torch.empty(0, device="cuda")
+    t = torch.empty(0, 8, device="cuda")
+    assert mse_loss_op(O, lse, t, None, 0.0, "none").shape == (0,)
+    assert mse_loss_op(O, lse, t, None, 0.0, "sum").item() == 0.0
+    assert torch.isnan(mse_loss_op(O, lse, t, None, 0.0, "mean"))       # 0 / 0, as sum() / numel()
+    assert torch.isnan(formula(O, lse, t, None, 0.0, "mean"))
