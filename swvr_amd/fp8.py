@@ -178,8 +178,11 @@ def softmax_readout_fp8(h, W, E, bias=None, *, logit_scale=1.0, w_q=None, chunk_
     V, D = E.shape
     hq, hs = quantize_tensor(h2)
     Wq, ws = w_q if w_q is not None else quantize_rows(W)
-    if Wq.shape != (V, hq.shape[1]) or Wq.dtype != E4M3 or ws.shape != (V,):
-        raise ValueError(f"w_q must be quantize_rows(W) of a [{V}, {W.shape[1]}] W")
+    if Wq.shape != (V, hq.shape[1]) or Wq.dtype != E4M3 or ws.shape != (V,) or Wq.device != h.device:
+        raise ValueError(f"w_q must be quantize_rows(W) of a [{V}, {W.shape[1]}] W on {h.device}")
+    # the kernels read dense rows of Kp bytes and fp32 scales
+    Wq = Wq.contiguous()
+    ws = ws.to(device=h.device, dtype=torch.float32).contiguous()
     chunk = int(chunk_size) if chunk_size else default_chunk_size()
     if chunk <= 0:
         raise ValueError(f"chunk_size must be positive, got {chunk}")

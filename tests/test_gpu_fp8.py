@@ -171,3 +171,16 @@ def test_fp8_edge_sizes_no_tokens_and_one_vocabulary_row():
     Wq, ws = fp8.quantize_rows(W)
     S = (fp8.dequantize(hq, hs) @ fp8.dequantize(Wq, ws).T).squeeze(1) + b
     assert rel_err(lse, S) < 1e-5
+
+
+def test_fp8_accepts_a_strided_quantised_W():
+    h, W, E, b = make(100, 64, 700, 16, seed=4)
+    Wq, ws = fp8.quantize_rows(W)
+    big = torch.zeros(700, 128, dtype=torch.uint8, device="cuda")
+    big[:, :64] = Wq.view(torch.uint8)
+    big = big.view(fp8.E4M3)                          # rows of 128 bytes, the first 64 used
+    O1, l1 = fp8.softmax_readout_fp8(h, W, E, b, w_q=(Wq, ws))
+    O2, l2 = fp8.softmax_readout_fp8(h, W, E, b, w_q=(big[:, :64], ws))
+    assert torch.equal(O1, O2) and torch.equal(l1, l2)
+    with pytest.raises(ValueError):
+        fp8.softmax_readout_fp8(h, W, E, b, w_q=(Wq[:, :48], ws))
