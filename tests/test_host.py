@@ -232,3 +232,23 @@ def test_abi_fp8_forward_checks_arguments_without_touching_the_device():
     assert call(ldh=72) == _lib.EINVAL          # leading dim not a multiple of 16
     assert call(D=200) == _lib.EDTYPE
     assert call(hs=None) == _lib.EINVAL and b"scale" in lib.swvr_last_error()
+
+
+def test_abi_fp8_backward_checks_arguments_without_touching_the_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    N, K, V, D = 64, 64, 500, 16
+    base = lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 256, 1)
+    f8 = lib.swvr_bwd_fp8_workspace_size(N, K, K, V, D, 256, 1)
+    assert f8 > base                                   # + e4m3 h over positions and the row factors
+    assert lib.swvr_bwd_fp8_workspace_size(N, K, K, V, 200, 256, 1) == 0   # D above 128
+    assert lib.swvr_bwd_fp8_workspace_size(N, K, 40, V, D, 256, 1) == 0    # K8 not a multiple of 16
+
+    def call(K8=64, ldhq=64, ldwq=64, hs=p, D=16):
+        return lib.swvr_bwd_fp8(N, K, V, D, p, K, p, K, p, D, None, 1.0, p, K8, ldhq, hs, p, ldwq, p,
+                                p, p, p, p, 256, p, _lib.BF16, None, 0, None, 0, None, p, 1 << 30, None)
+
+    assert call(K8=48, ldhq=48, ldwq=48) == _lib.EINVAL   # K8 below K
+    assert call(ldhq=72) == _lib.EINVAL
+    assert call(hs=None) == _lib.EINVAL and b"scale" in lib.swvr_last_error()
+    assert call(D=200) == _lib.EDTYPE
