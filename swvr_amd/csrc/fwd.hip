@@ -34,12 +34,14 @@ template <class T, int DP>
 struct FwdTile {
   static constexpr bool wide = sizeof(T) == 2;
   static constexpr bool narrow = wide && DP <= 64;
-  static constexpr int BV = wide ? (DP <= 64 ? 256 : 128) : 128;
-  static constexpr int BM = narrow ? 256 : wide ? (DP <= 128 ? 128 : 64) : 64;
-  static constexpr int WV = narrow ? 2 : wide ? (DP == 128 ? 2 : 4) : 2;
-  static constexpr int WT = narrow ? 4 : wide ? (DP == 128 ? 4 : 2) : 2;
+  // 2-byte dtypes: 128 x 64 waves (D <= 64), 64 x 64 (D = 128), 64 x 32 (D = 256): the widest
+  // whose score and acc^T accumulators fit beside the operands
+  static constexpr int BV = wide ? (DP <= 128 ? 256 : 128) : 128;
+  static constexpr int BM = narrow ? 256 : wide ? 128 : 64;
+  static constexpr int WV = narrow ? 2 : wide ? (DP == 128 ? 4 : 2) : 2;
+  static constexpr int WT = narrow ? 4 : wide ? (DP == 128 ? 2 : 4) : 2;
   static constexpr int NT = 64 * WV * WT;
-  static constexpr int NS = narrow ? 3 : kStages;  // LDS ring depth
+  static constexpr int NS = narrow || (wide && DP == 128) ? 3 : kStages;  // LDS ring depth (160 KB with E^T)
 };
 
 // The e4m3 forward (h and W in OCP e4m3, E and P in bf16): one k64 MFMA per
