@@ -1049,12 +1049,18 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
   const int b = blockIdx.x;
   if (b < p.n_dw) {
-    gemm_tile<T, true>(p, xcd_swizzle(b, p.n_dw), smem);
+    int r, c;
+    grouped_tile(b, p.n_dw / p.n_n, p.n_n, &r, &c);
+    gemm_tile<T, true>(p, r * p.n_n + c, smem);
   } else {
     // dh tiles of the active positions' row blocks only (the grid covers all
     // of N); the active tiles are spread over every XCD
     const int n_dh = min(p.n_dh, (p.n_act[0] + G::GM - 1) / G::GM * p.n_n);
-    if (b - p.n_dw < n_dh) gemm_tile<T, false>(p, xcd_swizzle(b - p.n_dw, n_dh), smem);
+    if (b - p.n_dw < n_dh) {
+      int r, c;
+      grouped_tile(b - p.n_dw, n_dh / p.n_n, p.n_n, &r, &c);
+      gemm_tile<T, false>(p, r * p.n_n + c, smem);
+    }
   }
 }
 
