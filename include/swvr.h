@@ -150,6 +150,18 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
                    float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tiling the backward uses for this shape (no reference counterpart; for
+ * tests and tuning).  Writes up to n_out of: [0] BM, the token block of the
+ * scores kernel; [1] BV, its vocabulary tile; [2] G, the token groups a
+ * vocabulary tile's token blocks are split over (one workgroup per group, so a
+ * workgroup walks ceil(active token blocks / G) blocks); [3] C, the vocabulary
+ * rows per chunk; [4] the number of chunks; [5] DP, the padded embedding
+ * width; [6] 1 if the narrow-embedding scores kernel (side tiles carried by
+ * its K ring) runs, else 0.  Returns the number of fields (7) or a negative
+ * SWVR_E* code. */
+int swvr_bwd_tiling(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk,
+                    int64_t* out, int n_out);
+
 /* Forward with h and W in OCP e4m3 (fp8; opt-in, outside the reference's
  * precision policy, which has no fp8 path).  h [N][ldh] and W [V][ldw] hold
  * e4m3 bytes: h = h_scale[0] * h_e4m3 and W[v] = w_scale[v] * W_e4m3[v]

@@ -37,6 +37,7 @@ SIGNATURES = {
     "swvr_bwd_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i]),
     "swvr_bwd": (_i, [_i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f,
                       _p, _p, _p, _p, _i64, _p, _i, _p, _i, _p, _i, _p, _p, _sz, _p]),
+    "swvr_bwd_tiling": (_i, [_i, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_int64), _i]),
     "swvr_fwd_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "swvr_fwd_fp8": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _f,
                           _p, _p, _p, _sz, _p]),
@@ -95,6 +96,17 @@ def ptr(t):
 
 def stream_of(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def bwd_tiling(dtype, N, K, V, D, chunk):
+    """The backward's tiling for this shape (swvr_bwd_tiling): dict with BM, BV, G, C,
+    n_chunks, DP and ring."""
+    lib = load()
+    out = (ctypes.c_int64 * 7)()
+    rc = lib.swvr_bwd_tiling(DTYPE_TAG[dtype], N, K, V, D, chunk, out, 7)
+    if rc < 0:
+        check(rc)
+    return dict(zip(("BM", "BV", "G", "C", "n_chunks", "DP", "ring"), list(out)))
 
 
 def kernel_timing(enable=None):

@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <cstddef>
 #include <mutex>
 #include <vector>
 
@@ -37,7 +38,14 @@ std::mutex g_tmu;
 bool g_timing = false;
 std::vector<TimedLaunch> g_launches;
 std::vector<hipEvent_t> g_pool;
-hipEvent_t g_pending[kNumKinds];
+// Start events of launches whose end is not yet recorded, keyed by (stream, kind):
+// launches of one kind on different streams (or threads) pair their own events.
+struct PendingLaunch {
+  hipStream_t stream;
+  int kind;
+  hipEvent_t start;
+};
+std::vector<PendingLaunch> g_pending;
 
 hipEvent_t take_event() {
   if (!g_pool.empty()) {
@@ -87,17 +95,24 @@ void timing_begin(int kind, hipStream_t stream) {
   if (!g_timing) return;
   std::lock_guard<std::mutex> lk(g_tmu);
   hipEvent_t e = take_event();
-  if (e && hipEventRecord(e, stream) == hipSuccess) g_pending[kind] = e;
+  if (e && hipEventRecord(e, stream) == hipSuccess) g_pending.push_back({stream, kind, e});
 }
 
 void timing_end(int kind, hipStream_t stream) {
   if (!g_timing) return;
   std::lock_guard<std::mutex> lk(g_tmu);
-  hipEvent_t s = g_pending[kind];
-  g_pending[kind] = nullptr;
-  if (!s) return;
-  hipEvent_t e = take_event();
-  if (e && hipEventRecord(e, stream) == hipSuccess) g_launches.push_back({kind, s, e});
+  // the latest unmatched start of this kind on this stream
+  for (size_t i = g_pending.size(); i-- > 0;) {
+    if (g_pending[i].stream != stream || g_pending[i].kind != kind) continue;
+    const hipEvent_t s = g_pending[i].start;
+    g_pending.erase(g_pending.begin() + (std::ptrdiff_t)i);
+    hipEvent_t e = take_event();
+    if (e && hipEventRecord(e, stream) == hipSuccess)
+      g_launches.push_back({kind, s, e});
+    else
+      g_pool.push_back(s);
+    return;
+  }
 }
 
 namespace {
@@ -282,6 +297,21 @@ size_t swvr_bwd_workspace_size_mixed(int dtype, int w_dtype, int64_t N, int64_t 
 
 size_t swvr_bwd_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, int need_gh) {
   return swvr_bwd_workspace_size_mixed(dtype, dtype, N, K, V, D, chunk, need_gh);
+}
+
+int swvr_bwd_tiling(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, int64_t* out, int n_out) {
+  g_err[0] = 0;
+  if (!out || n_out < 0) return fail(SWVR_EINVAL, "out must be non-null");
+  BwdPlan plan;
+  if (N < 0 || K < 0 || V < 0 || D < 0 || chunk <= 0)
+    return fail(SWVR_EINVAL, "bad sizes N=%lld K=%lld V=%lld D=%lld chunk=%lld", (long long)N, (long long)K,
+                (long long)V, (long long)D, (long long)chunk);
+  if (!bwd_plan(dtype, N, K, V, D, chunk, true, &plan))
+    return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  const int64_t v[7] = {plan.BM, plan.BV, plan.G, plan.C, plan.n_chunks, plan.DP, plan.ring};
+  const int n = n_out < 7 ? n_out : 7;
+  for (int i = 0; i < n; ++i) out[i] = v[i];
+  return 7;
 }
 
 int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,

@@ -1395,6 +1395,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G < 1) G = 1;
   plan->G = G;
   plan->n_gpart = G * WT;  // dE / db partials: one per token group and token-wave row
+  plan->ring = wgs == 256;
   plan->dh_acc = need_gh;
   plan->V_pad = ((V + BV - 1) / BV) * BV;
   const size_t tb = dtype_bytes(dtype);

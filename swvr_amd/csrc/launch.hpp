@@ -85,6 +85,7 @@ struct BwdPlan {
   int n_chunks;
   int G;                 // token groups of the dS kernel
   int n_gpart;           // dE / db partials per chunk
+  int ring;              // 1: the narrow-embedding scores kernel (side tiles carried by the K ring)
   bool dh_acc;           // dh accumulates in fp32 (over the active tokens), then expands into gh
   int V_pad;             // vocabulary rows of the packed E / bias
   int hS;                // reduction slices of the packed h and W

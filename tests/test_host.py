@@ -252,3 +252,19 @@ def test_abi_fp8_backward_checks_arguments_without_touching_the_device():
     assert call(ldhq=72) == _lib.EINVAL
     assert call(hs=None) == _lib.EINVAL and b"scale" in lib.swvr_last_error()
     assert call(D=200) == _lib.EDTYPE
+
+
+def test_bwd_tiling_reports_the_scores_kernel_plan():
+    """swvr_bwd_tiling needs no GPU: the headline's ring-kernel tiling and the general kernel's."""
+    t = _lib.bwd_tiling(torch.bfloat16, 16384, 2560, 151936, 64, 8192)
+    assert t == dict(BM=256, BV=256, G=8, C=8192, n_chunks=19, DP=64, ring=1)
+    t = _lib.bwd_tiling(torch.bfloat16, 32768, 4096, 256000, 256, 8192)
+    assert (t["BM"], t["BV"], t["G"], t["DP"], t["ring"]) == (64, 128, 8, 256, 0)
+    t = _lib.bwd_tiling(torch.float32, 2051, 64, 4096, 128, 4096)
+    assert (t["BM"], t["G"], t["C"], t["ring"]) == (64, 16, 4096, 0)
+    lib = _lib.load()
+    out = (ctypes.c_int64 * 7)()
+    assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 0, out, 7) == _lib.EINVAL
+    assert b"chunk" in lib.swvr_last_error()
+    assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 300, 64, out, 7) == _lib.EDTYPE
+    assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 64, None, 7) == _lib.EINVAL

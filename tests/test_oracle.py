@@ -85,6 +85,50 @@ def test_mse_matches_golden():
     close(got, T(c["mse_unweighted_mean"]))
 
 
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("block", [1, 2, 1024])
+def test_blocked_reference_matches_golden(name, block):
+    """The row-blocked evaluation the full-size GPU tests use gives the golden values."""
+    c = CASES[name]
+    h, W, E, b = inputs_of(c)
+    out = ref.reference_grads_blocked(h, W, E, b, T(c["gO"]), T(c["glse"]), c["logit_scale"], block=block)
+    for got, key in zip(out, ["O", "lse", "gh", "gW", "gE", "gb"]):
+        if c[key] is None:
+            assert got is None
+        else:
+            close(got, T(c[key]), rtol=1e-9, atol=1e-9)
+
+
+@pytest.mark.parametrize("reduction", ["sum", "mean"])
+@pytest.mark.parametrize("block", [1, 4, 1024])
+def test_blocked_mse_matches_golden_and_autograd(reduction, block):
+    c = CASES["mse"]
+    h, W, E, b = inputs_of(c)
+    t, w, z, s = T(c["target"]), T(c["weight"]), c["z_loss_weight"], c["logit_scale"]
+    loss, *grads = ref.mse_grads_blocked(h, W, E, t, b, weight=w, reduction=reduction, z_loss_weight=z,
+                                         logit_scale=s, block=block)
+    close(loss, T(c["mse"][reduction]))
+    xs = [x.clone().requires_grad_(True) for x in (h, W, E, b)]
+    want = torch.autograd.grad(ref.mse_reference(*xs[:3], t, xs[3], weight=w, reduction=reduction,
+                                                 z_loss_weight=z, logit_scale=s), xs)
+    for got, r in zip(grads, want):
+        close(got, r)
+    with pytest.raises(ValueError):
+        ref.mse_grads_blocked(h, W, E, t, b, reduction="none")
+
+
+def test_blocked_reference_has_no_cross_block_terms():
+    """A planted mistake: a block size that drops the last partial block must not pass."""
+    h, W, E, b = make(N=7)
+    gO, glse = torch.randn(7, 5, dtype=f64), torch.randn(7, dtype=f64)
+    full = ref.reference_grads(h, W, E, b, gO, glse)
+    blocked = ref.reference_grads_blocked(h, W, E, b, gO, glse, block=3)
+    for a, r in zip(blocked, full):
+        close(a, r)
+    dropped = ref.reference_grads_blocked(h[:6], W, E, b, gO[:6], glse[:6], block=3)
+    assert not torch.allclose(dropped[3], full[3])
+
+
 def make(N=6, K=12, V=41, D=5, dtype=f64, bias=True, seed=0):
     g = torch.Generator().manual_seed(seed)
     t = lambda *s: torch.randn(*s, generator=g, dtype=f64).to(dtype)
