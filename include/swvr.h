@@ -227,6 +227,22 @@ int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const 
                   int64_t ldt, const float* weight, float z_loss_weight, int reduction, float* out, float* scale,
                   float* gO, float* glse, void* workspace, size_t workspace_bytes, void* stream);
 
+/* swvr_mse_loss without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc).  No reference
+ * counterpart.  The per-workgroup partial sums go to a fixed array in device
+ * memory that each GPU the library runs on holds until the process ends
+ * (8 * ceil(N / 16) bytes used, 2 MiB in all), so N is at most
+ * SWVR_MSE_NOALLOC_MAX_N; larger N returns SWVR_EINVAL.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (several streams or
+ * threads at once) race and must be serialised by the caller.  Each call
+ * writes every partial it reads, so nothing needs clearing between calls.
+ * Arguments and results are those of swvr_mse_loss, bit for bit. */
+#define SWVR_MSE_NOALLOC_MAX_N (1 << 22)
+int swvr_mse_loss_noalloc(int64_t N, int64_t D, const float* O, const float* lse, const void* target,
+                          int target_dtype, int64_t ldt, const float* weight, float z_loss_weight, int reduction,
+                          float* out, float* scale, float* gO, float* glse, void* stream);
+
 /* Instrumentation (no reference counterpart).  While enabled, every kernel
  * launch is bracketed by a pair of HIP events on its stream.
  * swvr_timing_collect synchronises those events, writes per-kernel-kind total

@@ -48,6 +48,7 @@ SIGNATURES = {
     "swvr_quantize_e4m3": (_i, [_i64, _i64, _i64, _p, _i64, _i, _i, _p, _i64, _p, _p, _sz, _p]),
     "swvr_mse_loss_workspace_size": (_sz, [_i64]),
     "swvr_mse_loss": (_i, [_i64, _i64, _p, _p, _p, _i, _i64, _p, _f, _i, _p, _p, _p, _p, _p, _sz, _p]),
+    "swvr_mse_loss_noalloc": (_i, [_i64, _i64, _p, _p, _p, _i, _i64, _p, _f, _i, _p, _p, _p, _p, _p]),
     "swvr_timing_enable": (_i, [_i]),
     "swvr_timing_collect": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _i]),
     "swvr_kernel_name": (ctypes.c_char_p, [_i]),

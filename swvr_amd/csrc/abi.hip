@@ -517,6 +517,25 @@ int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const 
   return SWVR_OK;
 }
 
+int swvr_mse_loss_noalloc(int64_t N, int64_t D, const float* O, const float* lse, const void* target,
+                          int target_dtype, int64_t ldt, const float* weight, float z_loss_weight, int reduction,
+                          float* out, float* scale, float* gO, float* glse, void* stream) {
+  g_err[0] = 0;
+  static_assert(SWVR_MSE_NOALLOC_MAX_N == swvr::kMseNoAllocMaxTokens, "one limit");
+  if (N > SWVR_MSE_NOALLOC_MAX_N)
+    return fail(SWVR_EINVAL, "N=%lld exceeds the maximum %d of swvr_mse_loss_noalloc (use swvr_mse_loss)",
+                (long long)N, SWVR_MSE_NOALLOC_MAX_N);
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (N > 0 && reduction != SWVR_REDUCE_NONE) {
+    const hipError_t e = swvr::mse_noalloc_scratch(&ws);
+    if (e != hipSuccess) return hip_fail(e, "scratch address");
+    ws_bytes = swvr::mse_workspace_bytes((int)N);
+  }
+  return swvr_mse_loss(N, D, O, lse, target, target_dtype, ldt, weight, z_loss_weight, reduction, out, scale, gO,
+                       glse, ws, ws_bytes, stream);
+}
+
 const char* swvr_kernel_name(int kind) {
   if (kind < 0 || kind >= kNumKinds) return "";
   return kKindNames[kind];

@@ -155,6 +155,11 @@ struct MseParams {
   float* glse;          // [N] or null (with gO)
 };
 size_t mse_workspace_bytes(int N);
+// Largest N of the allocation-free loss entry point, whose partial sums live in
+// a fixed device array (loss.hip) instead of the caller's workspace.
+constexpr int kMseNoAllocMaxTokens = 1 << 22;
+// Address of that array on the current device (looked up once per device).
+hipError_t mse_noalloc_scratch(void** ptr);
 
 // ---------------------------------------------------------------- e4m3 quantisation
 struct QuantParams {

@@ -15,6 +15,8 @@
 // workgroup's sums of per_tok and w in token order.  mse_reduce_kernel: one
 // workgroup adds the partial sums in a fixed order, so the loss is the same
 // on every run.
+#include <mutex>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -117,7 +119,35 @@ hipError_t launch_token(const MseParams& p, int n_blk, float* part, hipStream_t 
   return hipGetLastError();
 }
 
+// Scratch of the allocation-free entry point (swvr_mse_loss_noalloc): the
+// per-workgroup partial sums of up to kMseNoAllocMaxTokens tokens.  Each device
+// holds its own copy for the life of the process; its address comes from
+// hipGetSymbolAddress (the name itself is a host-side stand-in in host code).
+constexpr int kNoAllocMaxBlocks = (kMseNoAllocMaxTokens + kLossTokensPerBlock - 1) / kLossTokensPerBlock;
+static __device__ __align__(256) float scratch[2 * kNoAllocMaxBlocks];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
+
+hipError_t mse_noalloc_scratch(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // the array on the current device
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
+}
 
 size_t mse_workspace_bytes(int N) {
   const int64_t n_blk = ((int64_t)N + kLossTokensPerBlock - 1) / kLossTokensPerBlock;
