@@ -156,9 +156,10 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
  * vocabulary tile's token blocks are split over (one workgroup per group, so a
  * workgroup walks ceil(active token blocks / G) blocks); [3] C, the vocabulary
  * rows per chunk; [4] the number of chunks; [5] DP, the padded embedding
- * width; [6] 1 if the narrow-embedding scores kernel (side tiles carried by
- * its K ring) runs, else 0.  Returns the number of fields (7) or a negative
- * SWVR_E* code. */
+ * width; [6] the scores kernel: 1 the narrow-embedding kernel (side tiles
+ * carried by its K ring), 2 the wide-embedding kernel (gO and E streamed as
+ * D-slices; dE formed by the gradient GEMM launch), 0 the general one.
+ * Returns the number of fields (7) or a negative SWVR_E* code. */
 int swvr_bwd_tiling(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk,
                     int64_t* out, int n_out);
 

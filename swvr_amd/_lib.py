@@ -101,13 +101,13 @@ def stream_of(device):
 
 def bwd_tiling(dtype, N, K, V, D, chunk):
     """The backward's tiling for this shape (swvr_bwd_tiling): dict with BM, BV, G, C,
-    n_chunks, DP and ring."""
+    n_chunks, DP and kernel (0 general, 1 narrow ring, 2 wide)."""
     lib = load()
     out = (ctypes.c_int64 * 7)()
     rc = lib.swvr_bwd_tiling(DTYPE_TAG[dtype], N, K, V, D, chunk, out, 7)
     if rc < 0:
         check(rc)
-    return dict(zip(("BM", "BV", "G", "C", "n_chunks", "DP", "ring"), list(out)))
+    return dict(zip(("BM", "BV", "G", "C", "n_chunks", "DP", "kernel"), list(out)))
 
 
 def kernel_timing(enable=None):

@@ -308,7 +308,7 @@ int swvr_bwd_tiling(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64
                 (long long)V, (long long)D, (long long)chunk);
   if (!bwd_plan(dtype, N, K, V, D, chunk, true, &plan))
     return fail(SWVR_EDTYPE, "no backward kernel for dtype %d, D=%lld", dtype, (long long)D);
-  const int64_t v[7] = {plan.BM, plan.BV, plan.G, plan.C, plan.n_chunks, plan.DP, plan.ring};
+  const int64_t v[7] = {plan.BM, plan.BV, plan.G, plan.C, plan.n_chunks, plan.DP, plan.kind};
   const int n = n_out < 7 ? n_out : 7;
   for (int i = 0; i < n; ++i) out[i] = v[i];
   return 7;

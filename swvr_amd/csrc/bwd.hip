@@ -195,11 +195,13 @@ struct ScoresParams {
   int C;                // chunk stride of the partials (multiple of BV)
   int n_tb, G, n_vtc;
   void* stage;          // dS in the compute dtype, tiled (stage_off)
+  void* pstage;         // P in the compute dtype, same layout (wide kernel: dE^T = gO^T P in the GEMM launch)
   int n_tb32;           // N_pad / 32: 32-token blocks of the stage
   float* part_dE;       // [G][DP][C]
   float* part_db;       // [G][C]
   int need_stage, need_dE, need_db;
   const int* n_act;     // active positions (device)
+  int DP;               // padded embedding width (wide kernel: D-slices of gO and E)
 };
 
 // ---------------------------------------------------------------- dS stage layout
@@ -732,6 +734,180 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   }
 }
 
+// ---------------------------------------------------------------- scores, wide embeddings
+// bf16 / f16 with DP >= 128: 128 tokens x 256 vocabulary rows per workgroup of
+// 8 waves (2 token halves x 4 vocabulary quarters, 64 x 64 each).  Per token
+// block the ring carries the nk K-slices of h and W (-> S), then the DP / 32
+// D-slices of gO and E (-> dP = gO E^T), all as uniform 24 KB stages, so no
+// side tile is pinned in LDS and the next block's slices keep streaming
+// through the epilogue.  The epilogue stages dS and P in the compute dtype (P
+// rounded as the reference rounds it for dE, swvr/triton_kernels.py:113);
+// dE^T = gO^T P is a product of the gradient GEMM launch over all active
+// positions, so no dE accumulator lives in registers; db is a per-wave
+// register partial.  LSE / delta sit in a double-buffered LDS strip, the bias
+// in registers.
+struct ScoresWideTile {
+  static constexpr int BM = 128, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
+};
+
+template <class T, int DP>
+__global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
+  typedef ScoresWideTile C;
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int BM = C::BM, BV = C::BV, NT = C::NT, NS = C::NS;
+  constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
+  typedef PackedKLoader<T, BM, kBK, NT> TA;  // h rows of the token block (packed)
+  typedef PackedKLoader<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile (packed)
+  typedef KTile<T, BM, kBK, NT> TG;          // gO rows of the token block, one D-slice
+  typedef KTile<T, BV, kBK, NT> TE;          // E rows of the vocabulary tile, one D-slice
+  static_assert(sizeof(T) == 2 && DP % kBK == 0, "2-byte dtypes, whole D-slices");
+  static_assert(TG::BYTES == TA::BYTES && TE::BYTES == TB::BYTES && TG::NI == TA::NI && TE::NI == TB::NI,
+                "K- and D-stages load the same bytes");
+  static_assert(!TA::PARTIAL && !TB::PARTIAL, "whole loads");
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;  // loads per thread per stage
+  constexpr int FT = WTR / 32, FV = WVR / 32;
+  constexpr int ND = DP / kBK;
+
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4];
+  const float* const sLD = reinterpret_cast<const float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
+
+  const int lane = lane_id(), w = wave_id();
+  const int wt = w / C::WV, wv = w % C::WV;
+  int vt, g;
+  grouped_tile(blockIdx.x, p.n_vtc, p.G, &vt, &g);
+  const int vl0 = vt * BV;      // first chunk-local row of this tile
+  const int vg0 = p.v0 + vl0;   // its global row
+  const int rows = p.cv - vl0;  // valid rows of this tile (may exceed BV)
+  // token blocks of the active positions only, split evenly over the groups
+  const int n_tb_act = min(p.n_tb, (p.n_act[0] + BM - 1) / BM);
+  const int tb_begin = (int)((int64_t)g * n_tb_act / p.G);
+  const int tb_end = (int)((int64_t)(g + 1) * n_tb_act / p.G);
+  const int n_blocks = tb_end - tb_begin;
+
+  float dbacc[FV], bvv[FV];
+#pragma unroll
+  for (int fv = 0; fv < FV; ++fv) {
+    dbacc[fv] = 0.f;
+    const int vl = wv * WVR + fv * 32 + (lane & 31);
+    bvv[fv] = vl < rows ? p.biasp[vg0 + vl] : kNegInf;
+  }
+
+  const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
+  const int per_blk = nk + ND;
+  const int total = n_blocks * per_blk;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsL = lds0 + NS * SB;
+  TA ta;
+  ta.setup(p.hp, tb_begin * BM, p.hS);
+  TB tw;
+  tw.setup(p.Wp, vg0, p.hS);
+  const T* const gOp = static_cast<const T*>(p.gOp);
+  TG tg;
+  tg.setup(gOp + (int64_t)tb_begin * BM * DP, DP, BM, DP);
+  TE te;
+  te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP);
+  // issue cursor over the walk: stage `issued` is (block is_blk, sub-stage
+  // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk.. the D-slices
+  int issued = 0, is_blk = 0, is_sub = 0, is_slot = 0;
+  auto issue_next = [&]() {
+    if (issued >= total) return;
+    const uint32_t st = lds0 + is_slot * SB;
+    const int n0 = (tb_begin + is_blk) * BM;
+    if (is_sub < nk) {
+      if (is_sub == 0) {
+        ta.rebase(n0);
+        // LSE and delta of the block into strip (block & 1), ahead of its slices
+        const int c = (int)threadIdx.x + opaque_zero();
+        if (c < BM / 2) {
+          const uint32_t off = c < BM / 4 ? (uint32_t)(n0 + 4 * c) * 4 : (uint32_t)(p.N_pad + n0 + 4 * (c - BM / 4)) * 4;
+          dma_batch1(make_rsrc(p.lsed), off, ldsL + (is_blk & 1) * (2 * BM * 4) + w * 1024);
+        }
+      }
+      ta.issue(st, is_sub * kBK);
+      tw.issue(st + TA::BYTES, is_sub * kBK);
+    } else {
+      if (is_sub == nk) tg.base = reinterpret_cast<const char*>(gOp + (int64_t)n0 * DP);
+      const int d0 = (is_sub - nk) * kBK;
+      tg.issue(st, d0);
+      te.issue(st + TA::BYTES, d0);
+    }
+    ++issued;
+    if (++is_sub == per_blk) {
+      is_sub = 0;
+      ++is_blk;
+    }
+    is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue_next();
+
+  f32x16_t sacc[FT][FV], dacc[FT][FV];
+  Ring<NS> ring{NS - 1, total};  // the first publish_next() moves to stage 0, slot 0
+  for (int blk = 0; blk < n_blocks; ++blk) {
+    const int n0 = (tb_begin + blk) * BM;
+    // slice 0 of the block: every wave has also finished the previous block's
+    // epilogue (its LSE / delta strip is free again)
+    ring.template publish_next<L>();
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
+    tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
+    ring.template publish_next<L>();  // D-slice 0
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv) dacc[ft][fv] = zero16();
+    tile_reduce<T, kBK, L>(dacc, tg, te, smem, SB, ring, ND, wt * WTR, wv * WVR, issue_next);
+
+    const float* sLe = sLD + (blk & 1) * (2 * BM);
+    const float* sDe = sLe + BM;
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv) {
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft) {
+        const int ln = lane + opaque_zero();  // offsets recomputed per block (see opaque_zero)
+        const int vl = wv * WVR + fv * 32 + (ln & 31);  // tile-local row of this lane
+        const int tr0 = wt * WTR + ft * 32;             // first token of the block
+        float dbs = 0.f;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
+          const int tl = tr0 + 8 * g4 + (ln >> 5) * 4;
+          const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
+          const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g4 + i;
+            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv[fv]) - lv[i]);
+            const float ds = pv * (dacc[ft][fv][r] - dv[i]);
+            dbs += ds;
+            sacc[ft][fv][r] = pv;
+            dacc[ft][fv][r] = ds;  // the gradient GEMMs apply the scale (swvr/chunked.py:143-144)
+          }
+        }
+        dbacc[fv] += dbs;
+        if (p.need_stage) store_ds_block<T>(dacc[ft][fv], p.stage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
+        if (p.need_dE) store_ds_block<T>(sacc[ft][fv], p.pstage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
+        sched_fence();
+      }
+    }
+  }
+  wait_vmcnt<0>();
+
+  if (p.need_db) {
+    const int gp = g * C::WT + wt;
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv) {
+      const int vc = vl0 + wv * WVR + fv * 32 + (lane & 31);  // chunk-local row
+      const float s = wave_sum32(dbacc[fv]);
+      if (lane < 32) p.part_db[(int64_t)gp * p.C + vc] = s;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- GEMMs
 struct GemmParams {
   const void* stage;  // tiled dS (stage_off)
@@ -751,6 +927,13 @@ struct GemmParams {
   int dh_first;
   float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
   const int* n_act;  // active positions (device): the reduction length of dW, the rows of dh
+  // dE^T = gO^T P over positions (wide scores kernel): n_de tiles, n_de_n of them along the chunk
+  int n_de, n_de_n;
+  const void* pstage;  // P, tiled like the dS stage
+  const void* gOp;     // gO over positions [N_pad][DP]
+  int DP;
+  float* part_dE;      // output dE^T [DP][C], fp32
+  int C;
 };
 
 // Store 4 fp32 values as OutT (one 16- or 8-byte buffer store at byte offset
@@ -1035,9 +1218,35 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   }
 }
 
-// One launch covers both gradient products of a chunk: blocks [0, n_dw) are
-// dW tiles, blocks [n_dw, n_dw + n_dh) dh tiles.  The dW tiles (the longer
-// reduction, over all tokens) are dealt first.
+// One tile of dE^T = gO^T P over the active positions (wide scores kernel):
+// rows d (A: gO over positions read transposed, in stage position order), columns
+// chunk-local vocabulary rows (B: the P stage), written as fp32 [DP][C].
+template <class T>
+__device__ __forceinline__ void gemm_tile_de(const GemmParams& p, int t, char* smem) {
+  typedef GemmTile<T> G;
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int GM = G::GM, GN = G::GN, NT = G::NT;
+  constexpr int FM = GM / (32 * G::WM), FN = GN / (32 * G::WN);
+  const int w = wave_id();
+  const int wm = w / G::WN, wn = w % G::WN;
+  const int mt = t / p.n_de_n, nt = t % p.n_de_n;
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = zero16();
+  PosRLoader<T, GM, kBK, NT> ta;
+  ta.setup(static_cast<const T*>(p.gOp) + mt * GM, p.DP, p.DP - mt * GM, p.N);
+  StageKLoader<T, GN, kBK, NT> tb;
+  tb.setup(p.pstage, nt * GN, p.cv - nt * GN, p.n_tb32);
+  gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (min(p.N, p.n_act[0]) + 31) & ~31, wm * (GM / G::WM),
+                            wn * (GN / G::WN));
+  gemm_store<G>(acc, 1.f, p.part_dE, nullptr, 0, p.DP, mt * GM, nt * GN, p.C, smem);
+}
+
+// One launch covers the gradient products of a chunk: blocks [0, n_dw) are
+// dW tiles, then n_de dE^T tiles (wide scores kernel only), then dh tiles.
+// The dW and dE^T tiles (reductions over all active positions) are dealt first.
 template <class T>
 __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p) {
   typedef GemmTile<T> G;
@@ -1047,18 +1256,26 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
                 "both A layouts stage the same bytes");
   static_assert(kStages * SB <= G::LDS_BYTES, "ring fits");
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
-  const int b = blockIdx.x;
+  int b = blockIdx.x;
   if (b < p.n_dw) {
     int r, c;
     grouped_tile(b, p.n_dw / p.n_n, p.n_n, &r, &c);
     gemm_tile<T, true>(p, r * p.n_n + c, smem);
-  } else {
+    return;
+  }
+  b -= p.n_dw;
+  if (b < p.n_de) {
+    gemm_tile_de<T>(p, b, smem);
+    return;
+  }
+  b -= p.n_de;
+  {
     // dh tiles of the active positions' row blocks only (the grid covers all
     // of N); the active tiles are spread over every XCD
     const int n_dh = min(p.n_dh, (p.n_act[0] + G::GM - 1) / G::GM * p.n_n);
-    if (b - p.n_dw < n_dh) {
+    if (b < n_dh) {
       int r, c;
-      grouped_tile(b - p.n_dw, n_dh / p.n_n, p.n_n, &r, &c);
+      grouped_tile(b, n_dh / p.n_n, p.n_n, &r, &c);
       gemm_tile<T, false>(p, r * p.n_n + c, smem);
     }
   }
@@ -1067,16 +1284,18 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
 // ---------------------------------------------------------------- dE / db
 // One thread per (row, d) of gE plus one per row of gb; consecutive threads
 // take consecutive rows, so the partial reads are coalesced.
+// G_de: partials of dE ([G_de][DP][C]; 1 when the gradient GEMM formed dE^T
+// whole), G: partials of db ([G][C]).
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict__ part_dE,
-                                                         const float* __restrict__ part_db, int G, int C, int DP,
-                                                         int v0, int cv, int D, void* gE, int gE_dtype,
+                                                         const float* __restrict__ part_db, int G_de, int G, int C,
+                                                         int DP, int v0, int cv, int D, void* gE, int gE_dtype,
                                                          float* gb) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t n_e = gE ? (int64_t)cv * D : 0;
   if (e < n_e) {
     const int d = (int)(e / cv), v = (int)(e % cv);
     float s = 0.f;
-    for (int g = 0; g < G; ++g) s += part_dE[((int64_t)g * DP + d) * C + v];
+    for (int g = 0; g < G_de; ++g) s += part_dE[((int64_t)g * DP + d) * C + v];
     store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, s);
   } else if (gb && e < n_e + cv) {
     const int v = (int)(e - n_e);
@@ -1111,17 +1330,29 @@ struct ScoresRing {
   static constexpr bool value = sizeof(T) == 2 && DP <= 64;
 };
 
+// bf16 / f16 with DP >= 128 (bf16 scores): the wide kernel, dE formed by the gradient GEMM.
+template <class T, int DP, bool F8 = false>
+struct ScoresWide {
+  static constexpr bool value = sizeof(T) == 2 && DP >= 128 && !F8;
+};
+
 template <class T, int DP, bool F8 = false>
 hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   if constexpr (ScoresRing<T, DP>::value) {
     typedef ScoresRingTile<T, DP> C;
-    if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
+    if (plan.BM != C::BM || plan.BV != C::BV || plan.kind != kScoresRing) return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
     bwd_scores_ring_kernel<T, DP, F8><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
     timing_end(kKindBwdScores, stream);
+  } else if constexpr (ScoresWide<T, DP, F8>::value) {
+    typedef ScoresWideTile C;
+    if (plan.BM != C::BM || plan.BV != C::BV || plan.kind != kScoresWide) return hipErrorInvalidValue;
+    timing_begin(kKindBwdScores, stream);
+    bwd_scores_wide_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    timing_end(kKindBwdScores, stream);
   } else {
     typedef ScoresTile<T, DP> C;
-    if (plan.BM != C::BM || plan.BV != C::BV) return hipErrorInvalidValue;
+    if (plan.BM != C::BM || plan.BV != C::BV || plan.kind != kScoresGeneral) return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
     bwd_scores_kernel<T, DP, F8><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
     timing_end(kKindBwdScores, stream);
@@ -1155,7 +1386,7 @@ hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStrea
 
 template <class T>
 hipError_t dispatch_gemm(const BwdPlan& plan, const GemmParams& gp, hipStream_t stream) {
-  const int blocks = gp.n_dw + gp.n_dh;
+  const int blocks = gp.n_dw + gp.n_de + gp.n_dh;
   if (blocks == 0) return hipSuccess;
   if (plan.GM != GemmTile<T>::GM || plan.GN != GemmTile<T>::GN) return hipErrorInvalidValue;
   timing_begin(kKindBwdGemm, stream);
@@ -1169,6 +1400,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   hipError_t e;
   char* ws = p.ws;
   T* stage = reinterpret_cast<T*>(ws + plan.off_stage);
+  T* pstage = plan.kind == kScoresWide ? reinterpret_cast<T*>(ws + plan.off_pstage) : nullptr;
   float* part_dE = reinterpret_cast<float*>(ws + plan.off_pe);
   float* part_db = reinterpret_cast<float*>(ws + plan.off_pb);
   float* dh_acc = plan.dh_acc ? reinterpret_cast<float*>(ws + plan.off_dh) : nullptr;
@@ -1269,6 +1501,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.G = plan.G;
     sp.n_vtc = (cv + plan.BV - 1) / plan.BV;
     sp.stage = stage;
+    sp.pstage = pstage;
     sp.n_tb32 = (int)(plan.N_pad / 32);
     sp.part_dE = part_dE;
     sp.part_db = part_db;
@@ -1276,9 +1509,11 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.need_dE = p.gE != nullptr;
     sp.need_db = p.gb != nullptr;
     sp.n_act = n_act;
+    sp.DP = plan.DP;
     if ((e = dispatch_scores<T>(plan, sp, stream)) != hipSuccess) return e;
 
-    if (need_stage) {
+    const bool gemm_de = pstage && p.gE;  // dE^T = gO^T P as tiles of the gradient GEMM launch
+    if (need_stage || gemm_de) {
       GemmParams gp;
       gp.stage = stage;
       gp.n_tb32 = (int)(plan.N_pad / 32);
@@ -1294,6 +1529,13 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.n_n = (p.K + plan.GN - 1) / plan.GN;
       gp.n_dw = p.gW ? ((cv + plan.GM - 1) / plan.GM) * gp.n_n : 0;
       gp.n_dh = p.gh ? ((p.N + plan.GM - 1) / plan.GM) * gp.n_n : 0;
+      gp.n_de_n = (cv + plan.GN - 1) / plan.GN;
+      gp.n_de = gemm_de ? ((plan.DP + plan.GM - 1) / plan.GM) * gp.n_de_n : 0;
+      gp.pstage = pstage;
+      gp.gOp = gOp;
+      gp.DP = plan.DP;
+      gp.part_dE = part_dE;
+      gp.C = (int)plan.C;
       gp.gW = p.gW;
       gp.gW_dtype = p.gW_dtype;
       gp.dh_acc = dh_acc;
@@ -1305,9 +1547,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if (p.gE || p.gb) {
       timing_begin(kKindBwdReduce, stream);
       const int64_t n_threads = (p.gE ? (int64_t)cv * p.D : 0) + (p.gb ? cv : 0);
-      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(part_dE, part_db, plan.n_gpart, (int)plan.C,
-                                                                            plan.DP, v0, cv, p.D, p.gE, p.gE_dtype,
-                                                                            p.gb);
+      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
+          part_dE, part_db, plan.kind == kScoresWide ? 1 : plan.n_gpart, plan.n_gpart, (int)plan.C, plan.DP, v0, cv,
+          p.D, p.gE, p.gE_dtype, p.gb);
       timing_end(kKindBwdReduce, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
@@ -1328,13 +1570,23 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
 // chunk should have: one per CU for the ring kernel (one fits a CU), two per
 // CU otherwise.
 template <class T, int DP>
-void scores_get(int* BM, int* BV, int* WT, int* wgs) {
+void scores_get(bool f8, int* BM, int* BV, int* WT, int* wgs, int* kind) {
   if constexpr (ScoresRing<T, DP>::value) {
     *BM = ScoresRingTile<T, DP>::BM;
     *BV = ScoresRingTile<T, DP>::BV;
     *WT = ScoresRingTile<T, DP>::WT;
     *wgs = 256;
+    *kind = kScoresRing;
+    return;
+  }
+  if (ScoresWide<T, DP>::value && !f8) {
+    *BM = ScoresWideTile::BM;
+    *BV = ScoresWideTile::BV;
+    *WT = ScoresWideTile::WT;
+    *wgs = 256;  // one workgroup per CU (its ring takes 96 KB of LDS)
+    *kind = kScoresWide;
   } else {
+    *kind = kScoresGeneral;
     *BM = ScoresTile<T, DP>::BM;
     *BV = ScoresTile<T, DP>::BV;
     *WT = ScoresTile<T, DP>::WT;
@@ -1343,12 +1595,12 @@ void scores_get(int* BM, int* BV, int* WT, int* wgs) {
 }
 
 template <class T>
-void scores_tile_of(int DP, int* BM, int* BV, int* WT, int* wgs) {
+void scores_tile_of(int DP, bool f8, int* BM, int* BV, int* WT, int* wgs, int* kind) {
   switch (DP) {
-    case 32: scores_get<T, 32>(BM, BV, WT, wgs); break;
-    case 64: scores_get<T, 64>(BM, BV, WT, wgs); break;
-    case 128: scores_get<T, 128>(BM, BV, WT, wgs); break;
-    default: scores_get<T, 256>(BM, BV, WT, wgs); break;
+    case 32: scores_get<T, 32>(f8, BM, BV, WT, wgs, kind); break;
+    case 64: scores_get<T, 64>(f8, BM, BV, WT, wgs, kind); break;
+    case 128: scores_get<T, 128>(f8, BM, BV, WT, wgs, kind); break;
+    default: scores_get<T, 256>(f8, BM, BV, WT, wgs, kind); break;
   }
 }
 
@@ -1363,14 +1615,14 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (K8 > 0 && (dtype != kBF16 || D > 128 || K8 % 16 != 0)) return false;
   const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
   if (DP == 0) return false;
-  int BM, BV, GM, GN, WT, wgs;
+  int BM, BV, GM, GN, WT, wgs, kind;
   if (dtype == kF32) {
     if (DP > 128) return false;
-    scores_tile_of<float>(DP, &BM, &BV, &WT, &wgs);
+    scores_tile_of<float>(DP, false, &BM, &BV, &WT, &wgs, &kind);
     GM = GemmTile<float>::GM;
     GN = GemmTile<float>::GN;
   } else if (dtype == kBF16 || dtype == kF16) {
-    scores_tile_of<bf16_t>(DP, &BM, &BV, &WT, &wgs);
+    scores_tile_of<bf16_t>(DP, K8 > 0, &BM, &BV, &WT, &wgs, &kind);
     GM = GemmTile<bf16_t>::GM;
     GN = GemmTile<bf16_t>::GN;
   } else {
@@ -1394,8 +1646,8 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G > plan->n_tb) G = plan->n_tb;
   if (G < 1) G = 1;
   plan->G = G;
-  plan->n_gpart = G * WT;  // dE / db partials: one per token group and token-wave row
-  plan->ring = wgs == 256;
+  plan->n_gpart = G * WT;  // db (and, but for the wide kernel, dE) partials: one per token group and token-wave row
+  plan->kind = kind;
   plan->dh_acc = need_gh;
   plan->V_pad = ((V + BV - 1) / BV) * BV;
   const size_t tb = dtype_bytes(dtype);
@@ -1403,7 +1655,9 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->off_stage = off;
   off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pe = off;
-  off += align256((size_t)plan->n_gpart * DP * c * 4);
+  off += align256((size_t)(kind == kScoresWide ? 1 : plan->n_gpart) * DP * c * 4);
+  plan->off_pstage = off;
+  if (kind == kScoresWide) off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pb = off;
   off += align256((size_t)plan->n_gpart * c * 4);
   plan->off_dh = off;

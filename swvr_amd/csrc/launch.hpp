@@ -85,7 +85,7 @@ struct BwdPlan {
   int n_chunks;
   int G;                 // token groups of the dS kernel
   int n_gpart;           // dE / db partials per chunk
-  int ring;              // 1: the narrow-embedding scores kernel (side tiles carried by the K ring)
+  int kind;              // scores kernel: kScoresGeneral, kScoresRing (narrow), kScoresWide
   bool dh_acc;           // dh accumulates in fp32 (over the active tokens), then expands into gh
   int V_pad;             // vocabulary rows of the packed E / bias
   int hS;                // reduction slices of the packed h and W
@@ -93,7 +93,11 @@ struct BwdPlan {
   size_t off_flag, off_idx, off_inv, off_nact, off_delta, off_hc, off_Wc, ws_bytes;
   int hS8;               // e4m3 scores: reduction slices of the packed e4m3 h and W (K8 / 2 pairs)
   size_t off_hqc, off_mult;
+  size_t off_pstage;     // P stage (wide scores kernel), the dS stage's layout
 };
+
+// Scores kernels of the backward (BwdPlan::kind).
+enum { kScoresGeneral = 0, kScoresRing = 1, kScoresWide = 2 };
 
 // w_f32: W is stored in fp32 and needs a row-major copy in the compute dtype
 // (the dh product reads W rows directly).

@@ -100,17 +100,17 @@ def run_case(h, W, E, b, gO, glse, chunk):
     return (O.reshape(N, D), lse.reshape(N), *grads)
 
 
-# (dtype, N, K, V, D, chunk): ring kernel (2-byte dtypes, D <= 64) and general kernel
-# (D = 128 / 256, fp32), token counts that leave a partial last block, vocabularies
+# (dtype, N, K, V, D, chunk): narrow ring kernel (2-byte dtypes, D <= 64), wide kernel
+# (2-byte dtypes, D = 128 / 256) and general kernel (fp32), token counts that leave a partial last block, vocabularies
 # with a partial last chunk, and a small chunk (G = 32) whose groups get 2 or 3 blocks.
 CASES = [
     ("ring-bf16-D64", bf16, 8192 + 77, 256, 8192 + 300, 64, 8192),
     ("ring-bf16-D16", bf16, 8192 + 256, 128, 8192, 16, 8192),
     ("ring-f16-D48", f16, 9000, 192, 4096 + 64, 48, 4096),
     ("ring-bf16-chunk2048", bf16, 16384 + 5, 128, 4096 + 17, 64, 2048),
-    ("general-bf16-D128", bf16, 4096 + 33, 256, 8192 + 128, 128, 8192),
-    ("general-f16-D200", f16, 2048 + 100, 128, 8192, 200, 8192),
-    ("general-bf16-D256", bf16, 2048 + 64, 256, 8192 + 40, 256, 8192),
+    ("wide-bf16-D128", bf16, 4096 + 33, 256, 8192 + 128, 128, 8192),
+    ("wide-f16-D200", f16, 2048 + 100, 128, 8192, 200, 8192),
+    ("wide-bf16-D256", bf16, 2048 + 64, 256, 8192 + 40, 256, 8192),
     ("general-f32-D64", f32, 2048 + 9, 128, 8192, 64, 8192),
     ("general-f32-D128", f32, 2048 + 3, 64, 4096, 128, 4096),
 ]
@@ -121,7 +121,7 @@ def test_multiblock_backward_matches_fp64_on_every_row(case):
     tag, dtype, N, K, V, D, chunk = case
     print("case", tag, flush=True)
     t = assert_multiblock(dtype, N, K, V, D, chunk)
-    assert t["ring"] == (1 if tag.startswith("ring") else 0), t
+    assert t["kernel"] == {"ring": 1, "wide": 2, "general": 0}[tag.split("-")[0]], t
     h, W, E, b = draw(N, K, V, D, dtype, seed=sum(map(ord, tag)), w_scale=3.0)
     g = torch.Generator(device="cuda").manual_seed(7)
     gO = torch.randn(N, D, device="cuda", generator=g)

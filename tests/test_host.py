@@ -257,11 +257,11 @@ def test_abi_fp8_backward_checks_arguments_without_touching_the_device():
 def test_bwd_tiling_reports_the_scores_kernel_plan():
     """swvr_bwd_tiling needs no GPU: the headline's ring-kernel tiling and the general kernel's."""
     t = _lib.bwd_tiling(torch.bfloat16, 16384, 2560, 151936, 64, 8192)
-    assert t == dict(BM=256, BV=256, G=8, C=8192, n_chunks=19, DP=64, ring=1)
+    assert t == dict(BM=256, BV=256, G=8, C=8192, n_chunks=19, DP=64, kernel=1)
     t = _lib.bwd_tiling(torch.bfloat16, 32768, 4096, 256000, 256, 8192)
-    assert (t["BM"], t["BV"], t["G"], t["DP"], t["ring"]) == (64, 128, 8, 256, 0)
+    assert (t["BM"], t["BV"], t["G"], t["DP"], t["kernel"]) == (128, 256, 8, 256, 2)
     t = _lib.bwd_tiling(torch.float32, 2051, 64, 4096, 128, 4096)
-    assert (t["BM"], t["G"], t["C"], t["ring"]) == (64, 16, 4096, 0)
+    assert (t["BM"], t["G"], t["C"], t["kernel"]) == (64, 16, 4096, 0)
     lib = _lib.load()
     out = (ctypes.c_int64 * 7)()
     assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 0, out, 7) == _lib.EINVAL
