@@ -83,19 +83,21 @@ def algorithmic_flops(N, K, V, D):
     return fwd, 2.0 * N * V * (4 * K + 3 * D)
 
 
-def kernel_flops(name, N, K, V, D, n_act=None):
+def kernel_flops(name, N, K, V, D, n_act=None, de_in_gemm=False):
     """Algorithmic FLOPs of all launches of one kernel kind over one step.
 
     The backward runs over the ``n_act`` tokens whose cotangents are not all
     zero (zero-weight tokens contribute nothing), so its kernels are priced on
-    the work they do: n_act tokens."""
+    the work they do: n_act tokens.  ``de_in_gemm``: the wide-embedding scores
+    kernel stages P and the gradient GEMM launch forms dE = P^T gO."""
     nb = N if n_act is None else n_act
     if name == "fwd_tile_kernel":
         return 2.0 * N * V * (K + D)             # S = h W^T, P E
     if name == "bwd_scores_kernel":
-        return 2.0 * nb * V * (K + 2 * D)        # S recompute, dP = gO E^T, dE = P^T gO
+        # S recompute, dP = gO E^T (and dE = P^T gO unless the GEMM launch forms it)
+        return 2.0 * nb * V * (K + (1 if de_in_gemm else 2) * D)
     if name == "bwd_gemm_kernel":
-        return 4.0 * nb * V * K                  # dh = dS W, dW = dS^T h
+        return 4.0 * nb * V * K + (2.0 * nb * V * D if de_in_gemm else 0.0)  # dh = dS W, dW = dS^T h (, dE)
     return 0.0
 
 
@@ -274,15 +276,16 @@ def main():
     # tokens with a non-zero weight: the others have zero cotangents, and the
     # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
     n_act = int((weight != 0).sum().item()) if weight is not None else N
+    de_in_gemm = _lib.bwd_tiling(torch.bfloat16, N, K, V, D, args.chunk)["kernel"] == 2
     per_kernel = {}
     for name, (kms, cnt) in kernels.items():
-        kf = kernel_flops(name, N, K, V, D, n_act) * args.steps
+        kf = kernel_flops(name, N, K, V, D, n_act, de_in_gemm) * args.steps
         per_kernel[name] = {"ms_per_step": round(kms / args.steps, 3), "launches_per_step": cnt // args.steps,
                             "avg_launch_ms": round(kms / cnt, 4),
                             "tflops": round(kf / (kms * 1e-3) / 1e12, 1) if kf else None}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     dk = per_kernel[dom]
-    launch_flops = kernel_flops(dom, N, K, V, D, n_act) * args.steps / (dk["launches_per_step"] * args.steps)
+    launch_flops = kernel_flops(dom, N, K, V, D, n_act, de_in_gemm) / dk["launches_per_step"]
     achieved = launch_flops / (dk["avg_launch_ms"] * 1e-3) / 1e12
     # W and E bytes the algorithm streams per step: fwd (W, E), bwd scores (W, E), dh GEMM (W)
     we_bytes = (3 * V * K + 2 * V * D) * 2

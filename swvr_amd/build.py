@@ -9,6 +9,7 @@ links against the HIP runtime only, not against torch.
 """
 import argparse
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -48,13 +49,69 @@ def _compile(src, obj, remarks):
     return r.stderr
 
 
+_FIELDS = {"VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch",
+           "Occupancy [waves/SIMD]": "occupancy", "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill",
+           "LDS Size [bytes/block]": "lds"}
+
+
+def resource_usage(remarks):
+    """Per-kernel register, scratch and LDS figures from hipcc's
+    -Rpass-analysis=kernel-resource-usage remarks: {mangled name: {field: int}}."""
+    out, cur = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z][^:]*?(?: \[[^\]]*\])?): (\d+)", line)
+        if m and cur is not None and m.group(1) in _FIELDS:
+            cur[_FIELDS[m.group(1)]] = int(m.group(2))
+    return out
+
+
+_TYPES = {"DF16b": "bf16", "DF16_": "f16", "f": "float"}
+
+
+def kernel_label(mangled):
+    """Short readable name of a kernel instantiation, e.g. ``fwd_tile_kernel<bf16,64,0>``
+    (template arguments of the Itanium-mangled name: types and integer literals)."""
+    m = re.match(r"_ZN4swvr(?:12_GLOBAL__N_1)?(\d+)", mangled)
+    if not m:
+        return mangled
+    n = int(m.group(1))
+    start = m.end()
+    name = mangled[start:start + n]
+    rest = mangled[start + n:]
+    if not rest.startswith("I"):
+        return name
+    args = []
+    for tok in re.finditer(r"DF16b|DF16_|L[a-z](\d+)E|(?<![A-Za-z])f", rest[1:rest.find("EE") + 1]):
+        t = tok.group(0)
+        args.append(tok.group(1) if t.startswith("L") else _TYPES[t])
+    return f"{name}<{','.join(args)}>"
+
+
+def resource_report():
+    """Compile every source with resource remarks into a scratch directory (the built library is
+    left as it is) and return {kernel label: resource usage}."""
+    with tempfile.TemporaryDirectory(prefix="swvr_remarks_") as tmp:
+        objs = [os.path.join(tmp, s + ".o") for s in SOURCES]
+        with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+            logs = list(ex.map(lambda a: _compile(a[0], a[1], True), zip(SOURCES, objs)))
+    usage = {}
+    for log in logs:
+        usage.update({kernel_label(k): v for k, v in resource_usage(log).items()})
+    return usage
+
+
 def build(remarks=False, verbose=False):
-    """Compile every source and link the shared library (atomically replaced)."""
+    """Compile every source and link the shared library (atomically replaced).
+    With remarks=True returns (path, {kernel: resource usage}) instead of the path."""
     with tempfile.TemporaryDirectory(prefix="swvr_build_") as tmp:
         objs = [os.path.join(tmp, s + ".o") for s in SOURCES]
         with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
             logs = list(ex.map(lambda a: _compile(a[0], a[1], remarks), zip(SOURCES, objs)))
-        if remarks or verbose:
+        if verbose:
             for s, log in zip(SOURCES, logs):
                 sys.stderr.write(f"---- {s}\n{log}")
         tmp_lib = os.path.join(tmp, LIB_NAME)
@@ -64,11 +121,25 @@ def build(remarks=False, verbose=False):
             raise RuntimeError(f"link failed:\n{r.stderr[-8000:]}")
         shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
         os.replace(LIB_PATH + ".tmp", LIB_PATH)
+    if remarks:
+        usage = {}
+        for log in logs:
+            usage.update(resource_usage(log))
+        return LIB_PATH, usage
     return LIB_PATH
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
-    ap.add_argument("--remarks", action="store_true")
+    ap.add_argument("--remarks", action="store_true", help="print registers, scratch and LDS per kernel")
     args = ap.parse_args()
-    print(build(remarks=args.remarks))
+    if args.remarks:
+        path, usage = build(remarks=True)
+        print(f"{'kernel':72s} {'vgpr':>5s} {'agpr':>5s} {'spill':>5s} {'scratch':>7s} {'occ':>3s} {'lds':>7s}")
+        for k in sorted(usage, key=kernel_label):
+            u = usage[k]
+            print(f"{kernel_label(k)[:72]:72s} {u.get('vgprs', 0):5d} {u.get('agprs', 0):5d} "
+                  f"{u.get('vgpr_spill', 0):5d} {u.get('scratch', 0):7d} {u.get('occupancy', 0):3d} {u.get('lds', 0):7d}")
+        print(path)
+    else:
+        print(build())

@@ -713,21 +713,24 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   }
   wait_vmcnt<0>();
 
-  // partials of this wave's rows over its token share of the group
-  const int gp = g * C::WT + wt;
+  // partials of this wave's rows over its token share of the group (thread
+  // offsets from an opaque thread index: computed here, not kept live through the walk)
+  const int to = (int)threadIdx.x + opaque_zero();
+  const int lo = to & 63, wo = to >> 6;
+  const int gp = g * C::WT + wo / C::WV;
 #pragma unroll
   for (int fv = 0; fv < FV; ++fv) {
-    const int vc = vl0 + wv * WVR + fv * 32 + (lane & 31);  // chunk-local row
+    const int vc = vl0 + (wo % C::WV) * WVR + fv * 32 + (lo & 31);  // chunk-local row
     if (p.need_db) {
       const float s = wave_sum32(dbacc[fv]);
-      if (lane < 32) p.part_db[(int64_t)gp * p.C + vc] = s;
+      if (lo < 32) p.part_db[(int64_t)gp * p.C + vc] = s;
     }
     if (p.need_dE) {
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int d = db * 32 + c_row(r, lane);
+          const int d = db * 32 + c_row(r, lo);
           p.part_dE[((int64_t)gp * DP + d) * p.C + vc] = deacc[db][fv][r];
         }
     }
@@ -966,8 +969,8 @@ __device__ __forceinline__ void store4(OutT* dst, float4 v) {
   }
 }
 
-// Write a GEMM tile through LDS: out[(row_off + row) * ld + col] = scale * acc
-// (+ prev[...]) for rows < rows, cols < ld, with the tile at (tile_row0,
+// Write a GEMM tile through LDS: out[(row_off + row) * ld + col] = fma(acc, scale,
+// prev[...]) (prev = 0 when null) for rows < rows, cols < ld, with the tile at (tile_row0,
 // tile_col0).  A lane's accumulators hold one column and 16 rows, so direct
 // stores would be 2- or 4-byte pieces; instead each half of the tile (the
 // rows of one wave row) is laid out row-major in LDS and written back by all
@@ -981,19 +984,24 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float 
   constexpr int HALF = G::GM / G::WM, LSTR = G::GN + 8;  // rows per pass, floats per LDS row
   static_assert(HALF * LSTR * 4 <= G::EPI_BYTES, "epilogue fits in LDS");
   float* lds = reinterpret_cast<float*>(smem);
-  const int lane = lane_id(), w = wave_id(), wm = w / G::WN, wn = w % G::WN;
+  // lane offsets from an opaque lane: computed here, not kept live through the reduction
+  const int lane = lane_id() + opaque_zero(), w = wave_id(), wm = w / G::WN, wn = w % G::WN;
 #pragma unroll
   for (int pass = 0; pass < G::WM; ++pass) {
     __syncthreads();  // every wave is done with the LDS (operand ring, or the previous pass)
     if (wm == pass) {
+      // register r of a block holds row c_row(r, lane) = 4 hi + 8 (r / 4) + r % 4 (hi = lane / 32),
+      // or for stage positions stage_tok of it = 8 hi + 16 ((r / 4) % 2) + 4 (r / 8) + r % 4:
+      // one lane base, and a compile-time offset per register
+      float* lb = lds + (POS ? 8 : 4) * (lane >> 5) * LSTR + wn * (G::GN / G::WN) + (lane & 31);
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int rl = fm * 32 + (POS ? stage_tok(c_row(r, lane)) : c_row(r, lane));
-            lds[rl * LSTR + wn * (G::GN / G::WN) + fn * 32 + (lane & 31)] = acc[fm][fn][r] * scale;
+            const int rc = POS ? 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3) : 8 * (r >> 2) + (r & 3);
+            lb[(fm * 32 + rc) * LSTR + fn * 32] = acc[fm][fn][r];
           }
     }
     __syncthreads();
@@ -1025,7 +1033,11 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[FM][FN], float 
     for (int i = 0; i < ITER; ++i) {
       const int c = i * G::NT + (int)threadIdx.x;
       float4 v = *reinterpret_cast<const float4*>(lds + (c / CPRW) * LSTR + (c % CPRW) * 4);
-      v.x += pv[i].x; v.y += pv[i].y; v.z += pv[i].z; v.w += pv[i].w;
+      // the scale is applied here, on the chunks being written, not to every accumulator at once
+      v.x = fmaf(v.x, scale, pv[i].x);
+      v.y = fmaf(v.y, scale, pv[i].y);
+      v.z = fmaf(v.z, scale, pv[i].z);
+      v.w = fmaf(v.w, scale, pv[i].w);
       store4_buf<OutT>(ro, el[i] == kOOB ? kOOB : el[i] * (uint32_t)sizeof(OutT), v);
     }
   }

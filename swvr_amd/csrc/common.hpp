@@ -42,7 +42,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kThreads = 256;  // every kernel here runs 4 waves of 64 lanes
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// Wave index in a 1-D workgroup: uniform across the wave, so it lives in a
+// scalar register (every wave-derived address with it).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // One k16 step of C += A * B on a 32x32 block.
 __device__ __forceinline__ void mfma_k16(f32x16_t& c, bf16x8_t a, bf16x8_t b) {
@@ -478,25 +480,28 @@ __global__ __launch_bounds__(256) void pack_vocab_kernel(const T* __restrict__ E
 template <class Tile, int F, int J>
 struct OpOffsets;
 
+// KTile: the chunk swizzle of a row repeats every 32 rows (chunk_swizzle), so
+// fragment f's operand sits 32 f rows (a compile-time byte offset, folded
+// into the LDS read's immediate) after fragment 0's: one register per step.
 template <class T, int R, int BK, int NT, int F, int J>
 struct OpOffsets<KTile<T, R, BK, NT>, F, J> {
   typedef KTile<T, R, BK, NT> KT;
   typedef typename Vec8<T>::type V8;
-  uint32_t off[J][F];
+  static constexpr uint32_t kFragBytes = 32 * KT::ROWB;
+  uint32_t off[J];
   __device__ __forceinline__ void init(int row0) {
     const int lane = lane_id();
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int f = 0; f < F; ++f) off[j][f] = KT::elem(row0 + 32 * f + (lane & 31), 16 * j + (lane >> 5) * 8);
+    for (int j = 0; j < J; ++j) off[j] = KT::elem(row0 + (lane & 31), 16 * j + (lane >> 5) * 8);
   }
   __device__ __forceinline__ V8 read(const char* stage, int j, int f) const {
     if constexpr (sizeof(T) == 2) {
-      return *reinterpret_cast<const V8*>(stage + off[j][f]);
+      return *reinterpret_cast<const V8*>(stage + off[j] + f * kFragBytes);
     } else {
       // 8 fp32 values span chunks c and c + 1 = c ^ 1 (c even): offsets o and o ^ 16
-      const float4 lo = *reinterpret_cast<const float4*>(stage + off[j][f]);
-      const float4 hi = *reinterpret_cast<const float4*>(stage + (off[j][f] ^ 16u));
+      // (kFragBytes is a multiple of 32, so the XOR commutes with the fragment offset)
+      const float4 lo = *reinterpret_cast<const float4*>(stage + off[j] + f * kFragBytes);
+      const float4 hi = *reinterpret_cast<const float4*>(stage + (off[j] ^ 16u) + f * kFragBytes);
       V8 v;
       v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
       v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
@@ -558,30 +563,28 @@ struct BRTile {
   static_assert(R % 32 == 0 && BYTES % (NT * 16) == 0, "whole sub-tiles, whole workgroup loads");
 };
 
+// BRTile: fragment f is sub-tile f after fragment 0's (a compile-time offset).
 template <class T, int R, int BK, int NT, int F, int J>
 struct OpOffsets<BRTile<T, R, BK, NT>, F, J> {
   typedef BRTile<T, R, BK, NT> BT;
   typedef typename Vec8<T>::type V8;
-  uint32_t off[F];
+  uint32_t off0;
   __device__ __forceinline__ void init(int row0) {
     const int lane = lane_id();
     if constexpr (sizeof(T) == 2) {
       // lane = 32 hi + 16 g + 4 a + q reads k-row 8 hi + a (+ 16 j + 4 h) at
       // rows 16 g + 4 q .. + 3 of sub-tile (row0 + 32 f) / 32
       const int hi = lane >> 5, g = (lane >> 4) & 1, a = (lane & 15) >> 2, q = lane & 3;
-#pragma unroll
-      for (int f = 0; f < F; ++f)
-        off[f] = (uint32_t)(((row0 + 32 * f) >> 5) * BT::SUB + (8 * hi + a) * BT::KROWB + (16 * g + 4 * q) * 2);
+      off0 = (uint32_t)((row0 >> 5) * BT::SUB + (8 * hi + a) * BT::KROWB + (16 * g + 4 * q) * 2);
     } else {
       // this lane's row (lane % 32) and first k-row (8 (lane / 32))
-#pragma unroll
-      for (int f = 0; f < F; ++f)
-        off[f] = (uint32_t)(((row0 + 32 * f) >> 5) * BT::SUB + 8 * (lane >> 5) * BT::KROWB + (lane & 31) * 4);
+      off0 = (uint32_t)((row0 >> 5) * BT::SUB + 8 * (lane >> 5) * BT::KROWB + (lane & 31) * 4);
     }
   }
   __device__ __forceinline__ V8 read(const char* stage, int j, int f) const {
+    const uint32_t off = off0 + f * BT::SUB;
     if constexpr (sizeof(T) == 2) {
-      const char* p = stage + off[f] + j * 16 * BT::KROWB;
+      const char* p = stage + off + j * 16 * BT::KROWB;
       const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
       const s16x4_t hi =
           __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p + 4 * BT::KROWB));
@@ -593,7 +596,7 @@ struct OpOffsets<BRTile<T, R, BK, NT>, F, J> {
       V8 out;
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        out[t] = *reinterpret_cast<const float*>(stage + off[f] + (16 * j + t) * BT::KROWB);
+        out[t] = *reinterpret_cast<const float*>(stage + off + (16 * j + t) * BT::KROWB);
       return out;
     }
   }

@@ -119,7 +119,7 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
   char* const sE = smem + NS * SB;
   const float* const sBias = reinterpret_cast<const float*>(sE + EBYTES);
 
-  const int lane = lane_id(), w = wave_id();
+  const int lane = lane_id(), w = (int)(threadIdx.x >> 6);
   const int wv = w / C::WT, wt = w % C::WT;
   int split, tb;
   grouped_tile(blockIdx.x, p.n_split, p.n_tb, &split, &tb);
@@ -284,12 +284,14 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
   }
 
   // ---- partial (m, l, acc) of this wave's vocabulary slice of this split
+  // (lane offsets from an opaque lane: computed here, not kept live through the loop)
   const int part = split * C::WV + wv;
+  const int ln = lane + opaque_zero();
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
-    const int n = n0 + wt * WTR + ft * 32 + (lane & 31);
+    const int n = n0 + wt * WTR + ft * 32 + (ln & 31);
     if (n < p.N) {
-      if (lane < 32) {
+      if (ln < 32) {
         p.part_m[(int64_t)part * p.N + n] = m[ft];
         p.part_l[(int64_t)part * p.N + n] = l[ft];
       }
@@ -297,7 +299,7 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int d = db * 32 + c_row(r, lane);
+          const int d = db * 32 + c_row(r, ln);
           p.part_acc[((int64_t)part * DP + d) * p.N + n] = oacc[db][ft][r];
         }
     }

@@ -1,0 +1,37 @@
+"""Compiler resource checks of the gfx950 kernels (no GPU needed: hipcc cross-compiles).
+
+A kernel that spills registers reads them back from scratch memory, and such a
+reload waits for every memory operation issued before it (vmcnt counts in
+issue order), stores included: in a kernel that streams dS out, one reload in
+the loop costs a full memory drain.  Every kernel must build without spills or
+scratch, and the hot ones within the LDS and occupancy their tiling assumes.
+"""
+import shutil
+
+import pytest
+
+from swvr_amd import build
+
+pytestmark = pytest.mark.skipif(shutil.which("hipcc") is None and not build.os.path.exists("/opt/rocm/bin/hipcc"),
+                                reason="hipcc not installed")
+
+
+@pytest.fixture(scope="module")
+def usage():
+    return build.resource_report()
+
+
+def test_no_kernel_spills_or_uses_scratch(usage):
+    assert usage, "no kernel resource remarks parsed"
+    bad = {k: v for k, v in usage.items() if v.get("vgpr_spill", 0) or v.get("sgpr_spill", 0) or v.get("scratch", 0)}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("kernel", ["fwd_tile_kernel<bf16,64,0>", "bwd_scores_ring_kernel<bf16,64,0>",
+                                    "bwd_gemm_kernel<bf16>", "bwd_scores_wide_kernel<bf16,256>",
+                                    "fwd_tile_kernel<bf16,256,0>"])
+def test_hot_kernels_run_two_waves_per_simd_within_lds(usage, kernel):
+    """The headline tiles are 8 waves of 512 threads: two waves per SIMD, one workgroup per CU."""
+    u = usage[kernel]
+    assert u["occupancy"] >= 2 and u["vgprs"] + u.get("agprs", 0) <= 256, u
+    assert u["lds"] <= 160 * 1024, u
