@@ -6,8 +6,10 @@ fake implementations for tracing and autograd wired through
 ``register_autograd``.  Their bodies call the HIP kernels through the C ABI
 (include/swvr.h) on the current stream; there is no other implementation.
 
-The reference op schemas carry a ``use_triton`` flag (chunked.py:157-161,
-170-174); this build has one code path, so the schemas here omit it.
+The schemas are the reference's (chunked.py:157-161, 170-174), ``use_triton``
+flag included, so graphs and callers written against them keep working.  The
+flag chose between the reference's Triton and torch elementwise paths; here
+both are the same HIP kernels, so it is accepted and has no effect.
 """
 from typing import List, Optional, Tuple
 
@@ -145,12 +147,13 @@ def _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, 
 
 @torch.library.custom_op("swvr::chunked_fwd", mutates_args=())
 def _fwd_op(h: torch.Tensor, W: torch.Tensor, E: torch.Tensor, bias: Optional[torch.Tensor],
-            logit_scale: float, chunk: int, cdt: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+            logit_scale: float, chunk: int, cdt: torch.dtype,
+            use_triton: bool) -> Tuple[torch.Tensor, torch.Tensor]:
     return _forward(h, W, E, bias, logit_scale, chunk, cdt)
 
 
 @_fwd_op.register_fake
-def _(h, W, E, bias, logit_scale, chunk, cdt):
+def _(h, W, E, bias, logit_scale, chunk, cdt, use_triton):
     adt = acc_dtype(cdt)
     return h.new_empty(h.shape[0], E.shape[1], dtype=adt), h.new_empty(h.shape[0], dtype=adt)
 
@@ -158,7 +161,7 @@ def _(h, W, E, bias, logit_scale, chunk, cdt):
 @torch.library.custom_op("swvr::chunked_bwd", mutates_args=())
 def _bwd_op(gO: torch.Tensor, glse: torch.Tensor, h: torch.Tensor, W: torch.Tensor, E: torch.Tensor,
             bias: Optional[torch.Tensor], O: torch.Tensor, lse: torch.Tensor, logit_scale: float,
-            chunk: int, cdt: torch.dtype, need_h: bool, need_W: bool, need_E: bool,
+            chunk: int, cdt: torch.dtype, use_triton: bool, need_h: bool, need_W: bool, need_E: bool,
             need_b: bool) -> List[torch.Tensor]:
     grads = _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt,
                       need_h, need_W, need_E, need_b)
@@ -167,16 +170,16 @@ def _bwd_op(gO: torch.Tensor, glse: torch.Tensor, h: torch.Tensor, W: torch.Tens
 
 
 @_bwd_op.register_fake
-def _(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, need_W, need_E, need_b):
+def _(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, use_triton, need_h, need_W, need_E, need_b):
     like = [(need_h, h), (need_W, W), (need_E, E), (need_b, bias)]
     return [torch.empty_like(x) if need else h.new_empty(0) for need, x in like]
 
 
 def _setup_context(ctx, inputs, output):
-    h, W, E, bias, logit_scale, chunk, cdt = inputs
+    h, W, E, bias, logit_scale, chunk, cdt, use_triton = inputs
     O, lse = output
     ctx.save_for_backward(h, W, E, bias, O, lse)
-    ctx.args = (logit_scale, chunk, cdt)
+    ctx.args = (logit_scale, chunk, cdt, use_triton)
 
 
 def _autograd_backward(ctx, gO, glse):
@@ -186,7 +189,7 @@ def _autograd_backward(ctx, gO, glse):
     gO = gO if gO is not None else torch.zeros_like(O)
     glse = glse if glse is not None else torch.zeros_like(lse)
     grads = _bwd_op(gO, glse, h, W, E, bias, O, lse, *ctx.args, *needs)
-    return (*[g if need else None for g, need in zip(grads, needs)], None, None, None)
+    return (*[g if need else None for g, need in zip(grads, needs)], None, None, None, None)
 
 
 _fwd_op.register_autograd(_autograd_backward, setup_context=_setup_context)
@@ -195,9 +198,9 @@ _fwd_op.register_autograd(_autograd_backward, setup_context=_setup_context)
 def softmax_readout_op(h2, W, E, bias, logit_scale, chunk, cdt):
     """``h2`` is ``[N, K]``; returns ``(O [N, D], LSE [N])`` in fp32 (swvr/chunked.py:208-212)."""
     if h2.device.type not in ("cuda", "cpu"):  # meta / fake tracing: no autocast state
-        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)
+        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt, True)
     with torch.autocast(h2.device.type, enabled=False):
-        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt)
+        return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt, True)
 
 
 # ---------------------------------------------------------------- fused MSE loss

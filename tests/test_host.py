@@ -168,9 +168,29 @@ def test_meta_tensors_trace_through_the_fake_kernels():
     O, lse = swvr_amd.softmax_readout(hb, Wb, Eb, bb)
     assert O.dtype == torch.float32   # scores, O and LSE stay fp32 for bf16 inputs
     grads = torch.ops.swvr.chunked_bwd(torch.empty(6, 5, device="meta"), torch.empty(6, device="meta"),
-                                       hb, Wb, Eb, bb, O, lse, 1.0, 8, torch.bfloat16, True, False, True, True)
+                                       hb, Wb, Eb, bb, O, lse, 1.0, 8, torch.bfloat16, True,
+                                       True, False, True, True)
     assert [tuple(g.shape) for g in grads] == [(6, 12), (0,), (41, 5), (41,)]
     assert grads[0].dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("use_triton", [True, False])
+def test_op_schemas_take_the_reference_argument_lists(use_triton):
+    """swvr::chunked_fwd / chunked_bwd with the reference's positional and keyword arguments
+    (swvr/chunked.py:157-161, 170-174), use_triton included; the flag has no effect here."""
+    hb, Wb, Eb, bb = (x.to(torch.bfloat16) for x in make(device="meta"))
+    O, lse = torch.ops.swvr.chunked_fwd(hb, Wb, Eb, bb, 1.0, 8, torch.bfloat16, use_triton)
+    assert O.shape == (6, 5) and lse.shape == (6,) and O.dtype == torch.float32
+    O2, _ = torch.ops.swvr.chunked_fwd(h=hb, W=Wb, E=Eb, bias=None, logit_scale=0.5, chunk=4,
+                                       cdt=torch.bfloat16, use_triton=use_triton)
+    assert O2.shape == (6, 5)
+    grads = torch.ops.swvr.chunked_bwd(gO=torch.empty(6, 5, device="meta"), glse=torch.empty(6, device="meta"),
+                                       h=hb, W=Wb, E=Eb, bias=bb, O=O, lse=lse, logit_scale=1.0, chunk=8,
+                                       cdt=torch.bfloat16, use_triton=use_triton, need_h=False, need_W=True,
+                                       need_E=False, need_b=True)
+    assert [tuple(g.shape) for g in grads] == [(0,), (41, 12), (0,), (41,)]
+    schema = str(torch.ops.swvr.chunked_fwd.default._schema)
+    assert "bool use_triton" in schema
 
 
 def test_drop_in_alias():
