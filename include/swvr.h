@@ -60,9 +60,13 @@ int swvr_abi_version(void);
  * swvr/api.py:14-22). */
 const char* swvr_last_error(void);
 
-/* Largest embedding width D supported for a dtype (256 for bf16/f16, 128 for
- * f32).  The reference's fused path has the same cap of 256
- * (swvr/triton_kernels.py:27). */
+/* Largest embedding width D supported for a dtype: SWVR_MAX_D for bf16, f16
+ * and f32, 0 for an unknown tag.  The reference has no cap (above 256 its
+ * fused kernels hand over to its torch path, swvr/triton_kernels.py:27,
+ * 121-123); here a forward with D above 256 (128 for f32) runs in passes over
+ * slices of E's columns, and the backward streams E and gO in D-slices.  The
+ * e4m3 entry points take D <= 128. */
+#define SWVR_MAX_D 65536
 int64_t swvr_max_d(int dtype);
 
 /* Workspace bytes swvr_fwd needs for this shape. */

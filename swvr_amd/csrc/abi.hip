@@ -237,8 +237,7 @@ int swvr_abi_version(void) { return SWVR_ABI_VERSION; }
 const char* swvr_last_error(void) { return g_err; }
 
 int64_t swvr_max_d(int dtype) {
-  if (dtype == SWVR_F32) return 128;
-  if (dtype == SWVR_BF16 || dtype == SWVR_F16) return 256;
+  if (dtype == SWVR_F32 || dtype == SWVR_BF16 || dtype == SWVR_F16) return SWVR_MAX_D;
   return 0;
 }
 

@@ -738,7 +738,8 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 }
 
 // ---------------------------------------------------------------- scores, wide embeddings
-// bf16 / f16 with DP >= 128: 128 tokens x 256 vocabulary rows per workgroup of
+// bf16 / f16 with DP > 64 and fp32 with DP > 128 (DP any multiple of the
+// slice width: 32 elements, 16 for fp32): 128 tokens x 256 vocabulary rows per workgroup of
 // 8 waves (2 token halves x 4 vocabulary quarters, 64 x 64 each).  Per token
 // block the ring carries the nk K-slices of h and W (-> S), then the DP / 32
 // D-slices of gO and E (-> dP = gO E^T), all as uniform 24 KB stages, so no
@@ -753,7 +754,7 @@ struct ScoresWideTile {
   static constexpr int BM = 128, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
 };
 
-template <class T, int DP>
+template <class T>
 __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   typedef ScoresWideTile C;
   constexpr int kBK = SliceK<T>::value;
@@ -763,14 +764,14 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   typedef PackedKLoader<T, BV, kBK, NT> TB;  // W rows of the vocabulary tile (packed)
   typedef KTile<T, BM, kBK, NT> TG;          // gO rows of the token block, one D-slice
   typedef KTile<T, BV, kBK, NT> TE;          // E rows of the vocabulary tile, one D-slice
-  static_assert(sizeof(T) == 2 && DP % kBK == 0, "2-byte dtypes, whole D-slices");
   static_assert(TG::BYTES == TA::BYTES && TE::BYTES == TB::BYTES && TG::NI == TA::NI && TE::NI == TB::NI,
                 "K- and D-stages load the same bytes");
   static_assert(!TA::PARTIAL && !TB::PARTIAL, "whole loads");
   constexpr int SB = TA::BYTES + TB::BYTES;
   constexpr int L = TA::NI + TB::NI;  // loads per thread per stage
   constexpr int FT = WTR / 32, FV = WVR / 32;
-  constexpr int ND = DP / kBK;
+  const int DP = p.DP;        // a multiple of the slice width kBK
+  const int ND = DP / kBK;    // D-slices per token block
 
   __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4];
   const float* const sLD = reinterpret_cast<const float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
@@ -1342,12 +1343,6 @@ struct ScoresRing {
   static constexpr bool value = sizeof(T) == 2 && DP <= 64;
 };
 
-// bf16 / f16 with DP >= 128 (bf16 scores): the wide kernel, dE formed by the gradient GEMM.
-template <class T, int DP, bool F8 = false>
-struct ScoresWide {
-  static constexpr bool value = sizeof(T) == 2 && DP >= 128 && !F8;
-};
-
 template <class T, int DP, bool F8 = false>
 hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   if constexpr (ScoresRing<T, DP>::value) {
@@ -1355,12 +1350,6 @@ hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_
     if (plan.BM != C::BM || plan.BV != C::BV || plan.kind != kScoresRing) return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
     bwd_scores_ring_kernel<T, DP, F8><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
-    timing_end(kKindBwdScores, stream);
-  } else if constexpr (ScoresWide<T, DP, F8>::value) {
-    typedef ScoresWideTile C;
-    if (plan.BM != C::BM || plan.BV != C::BV || plan.kind != kScoresWide) return hipErrorInvalidValue;
-    timing_begin(kKindBwdScores, stream);
-    bwd_scores_wide_kernel<T, DP><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
     timing_end(kKindBwdScores, stream);
   } else {
     typedef ScoresTile<T, DP> C;
@@ -1374,6 +1363,15 @@ hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_
 
 template <class T>
 hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
+  if (plan.kind == kScoresWide) {
+    typedef ScoresWideTile C;
+    if (sp.multp || plan.BM != C::BM || plan.BV != C::BV || plan.DP % SliceK<T>::value != 0)
+      return hipErrorInvalidValue;
+    timing_begin(kKindBwdScores, stream);
+    bwd_scores_wide_kernel<T><<<sp.n_vtc * sp.G, C::NT, 0, stream>>>(sp);
+    timing_end(kKindBwdScores, stream);
+    return hipGetLastError();
+  }
   if constexpr (std::is_same<T, bf16_t>::value) {
     if (sp.multp) {  // e4m3 scores (bf16 compute dtype only)
       switch (plan.DP) {
@@ -1385,12 +1383,11 @@ hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStrea
     }
   }
   if (sp.multp) return hipErrorInvalidValue;
-  switch (plan.DP) {
+  switch (plan.DP) {  // 2-byte dtypes: the ring kernel (DP <= 64); fp32: the general one (DP <= 128)
     case 32: return launch_scores<T, 32>(plan, sp, stream);
     case 64: return launch_scores<T, 64>(plan, sp, stream);
-    case 128: return launch_scores<T, 128>(plan, sp, stream);
-    case 256:
-      if constexpr (sizeof(T) == 2) return launch_scores<T, 256>(plan, sp, stream);
+    case 128:
+      if constexpr (sizeof(T) == 4) return launch_scores<T, 128>(plan, sp, stream);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -1579,41 +1576,14 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
 }
 
 // Tile of the scores kernel that serves (T, DP), and how many workgroups a
-// chunk should have: one per CU for the ring kernel (one fits a CU), two per
-// CU otherwise.
+// chunk should have: one per CU for the ring and wide kernels (one fits a
+// CU), two per CU for the general one.
 template <class T, int DP>
-void scores_get(bool f8, int* BM, int* BV, int* WT, int* wgs, int* kind) {
-  if constexpr (ScoresRing<T, DP>::value) {
-    *BM = ScoresRingTile<T, DP>::BM;
-    *BV = ScoresRingTile<T, DP>::BV;
-    *WT = ScoresRingTile<T, DP>::WT;
-    *wgs = 256;
-    *kind = kScoresRing;
-    return;
-  }
-  if (ScoresWide<T, DP>::value && !f8) {
-    *BM = ScoresWideTile::BM;
-    *BV = ScoresWideTile::BV;
-    *WT = ScoresWideTile::WT;
-    *wgs = 256;  // one workgroup per CU (its ring takes 96 KB of LDS)
-    *kind = kScoresWide;
-  } else {
-    *kind = kScoresGeneral;
-    *BM = ScoresTile<T, DP>::BM;
-    *BV = ScoresTile<T, DP>::BV;
-    *WT = ScoresTile<T, DP>::WT;
-    *wgs = 512;
-  }
-}
-
-template <class T>
-void scores_tile_of(int DP, bool f8, int* BM, int* BV, int* WT, int* wgs, int* kind) {
-  switch (DP) {
-    case 32: scores_get<T, 32>(f8, BM, BV, WT, wgs, kind); break;
-    case 64: scores_get<T, 64>(f8, BM, BV, WT, wgs, kind); break;
-    case 128: scores_get<T, 128>(f8, BM, BV, WT, wgs, kind); break;
-    default: scores_get<T, 256>(f8, BM, BV, WT, wgs, kind); break;
-  }
+void general_tile(int* BM, int* BV, int* WT, int* wgs) {
+  *BM = ScoresTile<T, DP>::BM;
+  *BV = ScoresTile<T, DP>::BV;
+  *WT = ScoresTile<T, DP>::WT;
+  *wgs = 512;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1624,22 +1594,48 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan,
               bool w_f32, int64_t K8) {
-  if (K8 > 0 && (dtype != kBF16 || D > 128 || K8 % 16 != 0)) return false;
-  const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
-  if (DP == 0) return false;
-  int BM, BV, GM, GN, WT, wgs, kind;
-  if (dtype == kF32) {
-    if (DP > 128) return false;
-    scores_tile_of<float>(DP, false, &BM, &BV, &WT, &wgs, &kind);
-    GM = GemmTile<float>::GM;
-    GN = GemmTile<float>::GN;
-  } else if (dtype == kBF16 || dtype == kF16) {
-    scores_tile_of<bf16_t>(DP, K8 > 0, &BM, &BV, &WT, &wgs, &kind);
-    GM = GemmTile<bf16_t>::GM;
-    GN = GemmTile<bf16_t>::GN;
+  const bool f8 = K8 > 0;
+  if (f8 && (dtype != kBF16 || D > 128 || K8 % 16 != 0)) return false;
+  const bool two = dtype == kBF16 || dtype == kF16;
+  if (!two && dtype != kF32) return false;
+  // Padded embedding width and scores kernel:
+  //   2-byte dtypes: the ring kernel up to 64; above, the wide kernel (any multiple of 32),
+  //     but the e4m3 scores, which keep the general kernel at 128;
+  //   fp32: the general kernel up to 128; above, the wide kernel (any multiple of 16).
+  int DP, kind;
+  if (D <= 64) {
+    DP = D <= 32 ? 32 : 64;
+    kind = two ? kScoresRing : kScoresGeneral;
+  } else if (f8 || (!two && D <= 128)) {
+    DP = 128;
+    kind = kScoresGeneral;
   } else {
-    return false;
+    const int64_t sw = two ? 32 : 16;
+    DP = (int)((D + sw - 1) / sw * sw);
+    kind = kScoresWide;
   }
+  int BM, BV, WT, wgs;
+  if (kind == kScoresRing) {
+    BM = ScoresRingTile<bf16_t, 64>::BM;
+    BV = ScoresRingTile<bf16_t, 64>::BV;
+    WT = ScoresRingTile<bf16_t, 64>::WT;
+    wgs = 256;
+  } else if (kind == kScoresWide) {
+    BM = ScoresWideTile::BM;
+    BV = ScoresWideTile::BV;
+    WT = ScoresWideTile::WT;
+    wgs = 256;  // one workgroup per CU (its ring takes 96 KB of LDS)
+  } else if (two) {
+    general_tile<bf16_t, 128>(&BM, &BV, &WT, &wgs);
+  } else if (DP == 32) {
+    general_tile<float, 32>(&BM, &BV, &WT, &wgs);
+  } else if (DP == 64) {
+    general_tile<float, 64>(&BM, &BV, &WT, &wgs);
+  } else {
+    general_tile<float, 128>(&BM, &BV, &WT, &wgs);
+  }
+  const int GM = two ? GemmTile<bf16_t>::GM : GemmTile<float>::GM;
+  const int GN = two ? GemmTile<bf16_t>::GN : GemmTile<float>::GN;
   plan->DP = DP;
   plan->BM = BM;
   plan->BV = BV;
@@ -1649,6 +1645,8 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->N_pad = ((N + 255) / 256) * 256;
   if (plan->N_pad == 0) plan->N_pad = 256;
   int64_t c = chunk < V ? chunk : V;
+  // at most 2^22 rows per chunk: tile-relative offsets into [DP or rows][C] buffers stay 32-bit
+  if (c > ((int64_t)1 << 22)) c = (int64_t)1 << 22;
   if (c < 1) c = 1;
   c = ((c + BV - 1) / BV) * BV;
   plan->C = c;

@@ -306,7 +306,7 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
   }
 }
 
-// Merge partial softmaxes in a fixed order: O = sum_p acc_p e^(m_p - M) /
+// Merge partial softmaxes in a fixed order (O rows ldo apart): O = sum_p acc_p e^(m_p - M) /
 // sum_p l_p e^(m_p - M), LSE = M + log(...).  A row with every score -inf ends
 // with M = -inf, L = 0: O = NaN and LSE = -inf, as swvr/chunked.py:105 gives.
 // Partial p of (row n, column d) of acc sits at p * sp + d * sd + n * sn, so
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_acc, int n_part, int N,
                                                           int D, int64_t sp, int64_t sd, int64_t sn,
-                                                          float* __restrict__ O, float* __restrict__ lse,
+                                                          float* __restrict__ O, int64_t ldo, float* __restrict__ lse,
                                                           float* __restrict__ m_out, float* __restrict__ l_out) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int Dw = D > 0 ? D : 1;
@@ -335,13 +335,13 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
     if (d < D) a += part_acc[q * sp + d * sd + n * sn] * wq;
   }
   if (m_out) {
-    if (d < D) O[(int64_t)n * D + d] = a;
+    if (d < D) O[(int64_t)n * ldo + d] = a;
     if (d == 0) {
       m_out[n] = M;
       l_out[n] = L;
     }
   } else {
-    if (d < D) O[(int64_t)n * D + d] = a / L;
+    if (d < D) O[(int64_t)n * ldo + d] = a / L;
     if (d == 0) lse[n] = M + logf(L);
   }
 }
@@ -398,14 +398,23 @@ void tile_of(int DP, int* BV, int* BM, int* WV) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// E^T tiles and the bias of one D-slice (p.E, p.D: the slice's columns).
 template <class T>
-hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
+hipError_t pack_et(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
   const int64_t n = (int64_t)plan.V_pad * plan.DP;
   timing_begin(kKindPack, stream);
   pack_et_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(
       static_cast<const T*>(p.E), p.lde, p.bias, p.V, p.D, plan.V_pad, plan.DP, plan.BV,
       const_cast<T*>(static_cast<const T*>(p.Ep)), const_cast<float*>(p.biasp), p.h_scale, p.w_scale, p.scale);
-  hipError_t e = hipGetLastError();
+  timing_end(kKindPack, stream);
+  return hipGetLastError();
+}
+
+// h and W in their tiles' LDS image, once per call.
+template <class T>
+hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
+  timing_begin(kKindPack, stream);
+  hipError_t e = hipSuccess;
   T* const hp = const_cast<T*>(static_cast<const T*>(p.hp));
   T* const Wp = const_cast<T*>(static_cast<const T*>(p.Wp));
   if (e == hipSuccess)
@@ -420,8 +429,14 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
 
 bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan) {
   (void)K;
-  const int DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0;
-  if (DP == 0) return false;
+  // Widest embedding slice of one pass: 256 (2-byte dtypes), 128 (fp32, e4m3).  A wider D runs
+  // in slices of that width, each pass recomputing the same scores for its columns of E.
+  const int DS = dtype == kBF16 || dtype == kF16 ? 256 : 128;
+  if (dtype == kFP8 && D > DS) return false;
+  const int64_t Dw = D < DS ? D : DS;
+  const int DP = Dw <= 32 ? 32 : Dw <= 64 ? 64 : Dw <= 128 ? 128 : 256;
+  plan->DS = DS;
+  plan->n_dslices = D > DS ? (int)((D + DS - 1) / DS) : 1;
   int BV, BM, WV;
   size_t tbytes;
   if (dtype == kF32) {
@@ -497,19 +512,37 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
   p.hS = plan.hS;
   hipError_t e;
   switch (dtype) {
-    case kBF16: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, p, stream); break;
-    case kF16: e = pack<f16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<f16_t>(plan, p, stream); break;
-    case kF32: e = pack<float>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp<float>(plan, p, stream); break;
-    case kFP8: e = pack<bf16_t>(p, plan, stream); if (e == hipSuccess) e = dispatch_dp_f8(plan, p, stream); break;
+    case kBF16: e = pack<bf16_t>(p, plan, stream); break;
+    case kF16: e = pack<f16_t>(p, plan, stream); break;
+    case kF32: e = pack<float>(p, plan, stream); break;
+    case kFP8: e = pack<bf16_t>(p, plan, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
-  timing_begin(kKindFwdCombine, stream);
-  const int64_t n_threads = (int64_t)p.N * (p.D > 0 ? p.D : 1);
-  fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
-      p.part_m, p.part_l, p.part_acc, plan.n_part, p.N, p.D, (int64_t)plan.DP * p.N, p.N, 1, O, lse, m_out, l_out);
-  timing_end(kKindFwdCombine, stream);
-  return hipGetLastError();
+  // one pass per slice of E's columns (one pass unless D exceeds the slice width)
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  const int D = p.D;
+  for (int d0 = 0; d0 < (D > 0 ? D : 1); d0 += plan.DS) {
+    FwdParams q = p;
+    q.E = static_cast<const char*>(p.E) + d0 * esz;
+    q.D = D - d0 < plan.DS ? D - d0 : plan.DS;
+    switch (dtype) {
+      case kBF16: e = pack_et<bf16_t>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, q, stream); break;
+      case kF16: e = pack_et<f16_t>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<f16_t>(plan, q, stream); break;
+      case kF32: e = pack_et<float>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<float>(plan, q, stream); break;
+      default: e = pack_et<bf16_t>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp_f8(plan, q, stream); break;
+    }
+    if (e != hipSuccess) return e;
+    // every pass computes the same scores, so each writes the same lse (m, l); O gets its columns
+    timing_begin(kKindFwdCombine, stream);
+    const int64_t n_threads = (int64_t)p.N * (q.D > 0 ? q.D : 1);
+    fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
+        p.part_m, p.part_l, p.part_acc, plan.n_part, p.N, q.D, (int64_t)plan.DP * p.N, p.N, 1, O ? O + d0 : nullptr,
+        D, lse, m_out, l_out);
+    timing_end(kKindFwdCombine, stream);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t shard_combine(int S, int N, int D, const float* m, const float* l, const float* acc, float* O, float* lse,
@@ -518,7 +551,7 @@ hipError_t shard_combine(int S, int N, int D, const float* m, const float* l, co
   if (n_threads == 0) return hipSuccess;
   timing_begin(kKindFwdCombine, stream);
   fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(m, l, acc, S, N, D, (int64_t)N * D, 1, D, O,
-                                                                         lse, nullptr, nullptr);
+                                                                         D, lse, nullptr, nullptr);
   timing_end(kKindFwdCombine, stream);
   return hipGetLastError();
 }

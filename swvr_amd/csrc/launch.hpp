@@ -53,6 +53,7 @@ struct FwdParams {
 
 struct FwdPlan {
   int BV, BM, DP;
+  int DS, n_dslices;     // embedding columns per pass, passes (D > DS runs in slices of E's columns)
   int n_tb, n_vt, n_split, n_part;
   int V_pad;
   int64_t N_pad;         // token rows of the packed h

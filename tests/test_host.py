@@ -34,8 +34,9 @@ def test_library_exports_every_declared_symbol():
 def test_abi_constants():
     lib = _lib.load()
     assert lib.swvr_abi_version() == _lib.ABI_VERSION
-    assert lib.swvr_max_d(_lib.BF16) == 256 and lib.swvr_max_d(_lib.F16) == 256
-    assert lib.swvr_max_d(_lib.F32) == 128 and lib.swvr_max_d(9) == 0
+    for tag in (_lib.BF16, _lib.F16, _lib.F32):
+        assert lib.swvr_max_d(tag) == 65536   # no practical cap: wide D runs in slices
+    assert lib.swvr_max_d(9) == 0
     assert lib.swvr_kernel_name(0).decode() == "fwd_tile_kernel"
     assert lib.swvr_kernel_name(99) == b""
 
@@ -51,7 +52,10 @@ def test_workspace_sizes():
     need = N * 8192 * 2 + N * K * 4 + (2 * N + V) * K * 2
     assert need <= bwd < need + 2**27
     assert lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 0, 1) == 0
-    assert lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 256) == 0   # fp32 caps D at 128
+    # a forward wider than one pass (256; fp32 128) reuses one pass's workspace for every slice
+    assert lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 300) == lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 128)
+    assert lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, 600) == lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, 256)
+    assert lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, 300, 8192, 1) > bwd
 
 
 def call_fwd(dtype=_lib.BF16, N=4, K=16, V=8, D=4, h=16, ldh=16, W=16, ldw=16, E=16, lde=4):
@@ -67,8 +71,8 @@ def call_fwd(dtype=_lib.BF16, N=4, K=16, V=8, D=4, h=16, ldh=16, W=16, ldw=16, E
     (dict(ldh=8), _lib.EINVAL),                     # ldh < K
     (dict(h=8), _lib.EINVAL),                       # misaligned h
     (dict(W=0), _lib.EINVAL),                       # null W
-    (dict(D=300, lde=300), _lib.EDTYPE),            # D above the bf16 cap
-    (dict(dtype=_lib.F32, D=200, lde=200), _lib.EDTYPE),
+    (dict(D=65537, lde=65537), _lib.EDTYPE),        # D above SWVR_MAX_D
+    (dict(dtype=_lib.F32, D=65537, lde=65537), _lib.EDTYPE),
     (dict(N=-1), _lib.EINVAL),
     (dict(K=(1 << 21) + 8, ldh=(1 << 21) + 8, ldw=(1 << 21) + 8), _lib.EINVAL),  # K above the 32-bit offset cap
 ])
@@ -274,6 +278,13 @@ def test_abi_fp8_backward_checks_arguments_without_touching_the_device():
     assert call(D=200) == _lib.EDTYPE
 
 
+def test_embedding_widths_beyond_the_maximum_are_refused():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    rc = lib.swvr_fwd(_lib.BF16, 4, 16, 8, 65537, p, 16, p, 16, p, 65537, None, 1.0, p, p, p, 1 << 20, None)
+    assert rc == _lib.EDTYPE and b"D=65537" in lib.swvr_last_error()
+
+
 def test_bwd_tiling_reports_the_scores_kernel_plan():
     """swvr_bwd_tiling needs no GPU: the headline's ring-kernel tiling and the general kernel's."""
     t = _lib.bwd_tiling(torch.bfloat16, 16384, 2560, 151936, 64, 8192)
@@ -282,9 +293,14 @@ def test_bwd_tiling_reports_the_scores_kernel_plan():
     assert (t["BM"], t["BV"], t["G"], t["DP"], t["kernel"]) == (128, 256, 8, 256, 2)
     t = _lib.bwd_tiling(torch.float32, 2051, 64, 4096, 128, 4096)
     assert (t["BM"], t["G"], t["C"], t["kernel"]) == (64, 16, 4096, 0)
+    # beyond the old caps: the wide kernel streams any multiple of 32 (fp32: 16) columns
+    assert (_lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 300, 512)["DP"], _lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 300, 512)["kernel"]) == (320, 2)
+    assert _lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 100, 512)["DP"] == 128
+    t = _lib.bwd_tiling(torch.float32, 64, 64, 512, 200, 512)
+    assert (t["DP"], t["kernel"]) == (208, 2)
     lib = _lib.load()
     out = (ctypes.c_int64 * 7)()
     assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 0, out, 7) == _lib.EINVAL
     assert b"chunk" in lib.swvr_last_error()
-    assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 300, 64, out, 7) == _lib.EDTYPE
+    assert lib.swvr_bwd_tiling(9, 16, 16, 16, 16, 64, out, 7) == _lib.EDTYPE
     assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 64, None, 7) == _lib.EINVAL
