@@ -154,6 +154,23 @@ int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    void* gh, int gh_dtype, void* gW, int gW_dtype, void* gE, int gE_dtype,
                    float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The readout in fp64 (no reference counterpart as an entry point: the
+ * reference computes fp64 inputs in fp64 on its torch path and returns fp64
+ * O / lse, swvr/chunked.py:26-27, 62-63).  Same quantities as swvr_fwd /
+ * swvr_bwd with every operand, bias, output and gradient fp64 and every
+ * stride in elements (no alignment or K-multiple rules; K < 2^22).  The
+ * vocabulary is processed `chunk` rows at a time, as the reference's chunk
+ * size: the workspace is O(N * chunk).  Gradients are deterministic. */
+size_t swvr_fwd_f64_workspace_size(int64_t N, int64_t V, int64_t D, int64_t chunk);
+int swvr_fwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, int64_t ldh, const double* W,
+                 int64_t ldw, const double* E, int64_t lde, const double* bias, double logit_scale, int64_t chunk,
+                 double* O, double* lse, void* workspace, size_t workspace_bytes, void* stream);
+size_t swvr_bwd_f64_workspace_size(int64_t N, int64_t V, int64_t D, int64_t chunk);
+int swvr_bwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, int64_t ldh, const double* W,
+                 int64_t ldw, const double* E, int64_t lde, const double* bias, double logit_scale, const double* O,
+                 const double* lse, const double* gO, const double* glse, int64_t chunk, double* gh, double* gW,
+                 double* gE, double* gb, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Tiling the backward uses for this shape (no reference counterpart; for
  * tests and tuning).  Writes up to n_out of: [0] BM, the token block of the
  * scores kernel; [1] BV, its vocabulary tile; [2] G, the token groups a

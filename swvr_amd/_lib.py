@@ -37,6 +37,12 @@ SIGNATURES = {
     "swvr_bwd_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64, _i64, _i]),
     "swvr_bwd": (_i, [_i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f,
                       _p, _p, _p, _p, _i64, _p, _i, _p, _i, _p, _i, _p, _p, _sz, _p]),
+    "swvr_fwd_f64_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "swvr_fwd_f64": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, ctypes.c_double, _i64,
+                          _p, _p, _p, _sz, _p]),
+    "swvr_bwd_f64_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "swvr_bwd_f64": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, ctypes.c_double, _p, _p, _p, _p,
+                          _i64, _p, _p, _p, _p, _p, _sz, _p]),
     "swvr_bwd_tiling": (_i, [_i, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_int64), _i]),
     "swvr_fwd_fp8_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "swvr_fwd_fp8": (_i, [_i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _f,

@@ -22,8 +22,8 @@ DEFAULT_CHUNK = 8192
 
 
 def acc_dtype(cdt):
-    """Accumulation / output dtype (swvr/chunked.py:26-27): fp32 here, as fp64 is not supported."""
-    return torch.float32
+    """Accumulation / output dtype (swvr/chunked.py:26-27): fp64 for an fp64 compute dtype, else fp32."""
+    return torch.float64 if cdt == torch.float64 else torch.float32
 
 
 def _require_device(t):
@@ -71,11 +71,65 @@ def _lead_stride(x):
     return x.stride(0) if x.shape[0] > 1 else x.shape[1]
 
 
+def _f64(x):
+    """``x`` in fp64 with unit stride in its last dimension (or None)."""
+    if x is None:
+        return None
+    x = x.to(torch.float64)
+    return x if x.dim() < 2 or x.stride(-1) == 1 else x.contiguous()
+
+
+def _forward_f64(h, W, E, bias, logit_scale, chunk):
+    """fp64 readout (swvr_fwd_f64): fp64 O and lse, as the reference returns for fp64 inputs."""
+    lib = _lib.load()
+    hd, Wd, Ed, bd = _f64(h), _f64(W), _f64(E), _f64(bias)
+    N, K = hd.shape
+    V, D = Ed.shape
+    O = torch.empty(N, D, dtype=torch.float64, device=h.device)
+    lse = torch.empty(N, dtype=torch.float64, device=h.device)
+    ws_bytes = lib.swvr_fwd_f64_workspace_size(N, V, D, int(chunk))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
+    with torch.cuda.device(h.device):
+        rc = lib.swvr_fwd_f64(N, K, V, D, _lib.ptr(hd), _lead_stride(hd), _lib.ptr(Wd), _lead_stride(Wd),
+                              _lib.ptr(Ed), _lead_stride(Ed), _lib.ptr(bd), float(logit_scale), int(chunk),
+                              _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_of(h.device))
+    _lib.check(rc)
+    return O, lse
+
+
+def _backward_f64(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, need_h, need_W, need_E, need_b):
+    lib = _lib.load()
+    hd, Wd, Ed, bd = _f64(h), _f64(W), _f64(E), _f64(bias)
+    N, K = hd.shape
+    V, D = Ed.shape
+    dev = h.device
+    f64 = torch.float64
+    gh = torch.empty(N, K, dtype=f64, device=dev) if need_h else None
+    gW = torch.empty(V, K, dtype=f64, device=dev) if need_W else None
+    gE = torch.empty(V, D, dtype=f64, device=dev) if need_E else None
+    gb = torch.empty(V, dtype=f64, device=dev) if need_b else None
+    gOd, glsed = gO.to(f64).contiguous(), glse.to(f64).contiguous()
+    Od, lsed = O.to(f64).contiguous(), lse.to(f64).contiguous()
+    ws_bytes = lib.swvr_bwd_f64_workspace_size(N, V, D, int(chunk))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.swvr_bwd_f64(N, K, V, D, _lib.ptr(hd), _lead_stride(hd), _lib.ptr(Wd), _lead_stride(Wd),
+                              _lib.ptr(Ed), _lead_stride(Ed), _lib.ptr(bd), float(logit_scale), _lib.ptr(Od),
+                              _lib.ptr(lsed), _lib.ptr(gOd), _lib.ptr(glsed), int(chunk), _lib.ptr(gh), _lib.ptr(gW),
+                              _lib.ptr(gE), _lib.ptr(gb), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev))
+    _lib.check(rc)
+    # gradients in the parameters' own dtypes (the reference's gH.to(h.dtype), empty_like(W), ...)
+    cast = lambda g, x: g.to(x.dtype) if g is not None and g.dtype != x.dtype else g
+    return cast(gh, h), cast(gW, W), cast(gE, E), cast(gb, bias)
+
+
 def _forward(h, W, E, bias, logit_scale, chunk, cdt):
     _require_device(h)
+    if cdt == torch.float64:
+        return _forward_f64(h, W, E, bias, logit_scale, chunk)
     lib = _lib.load()
     if cdt not in _lib.DTYPE_TAG:
-        raise NotImplementedError(f"swvr_amd: compute dtype {cdt} is not supported (bf16, fp16, fp32)")
+        raise NotImplementedError(f"swvr_amd: compute dtype {cdt} is not supported (bf16, fp16, fp32, fp64)")
     N, K = h.shape
     V, D = E.shape
     Kp = _kpad(K)
@@ -103,6 +157,8 @@ def _grad_buffer(shape, want, device):
 
 def _backward(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, cdt, need_h, need_W, need_E, need_b):
     _require_device(h)
+    if cdt == torch.float64:
+        return _backward_f64(gO, glse, h, W, E, bias, O, lse, logit_scale, chunk, need_h, need_W, need_E, need_b)
     lib = _lib.load()
     N, K = h.shape
     V, D = E.shape

@@ -1,9 +1,9 @@
-"""Public entry points: ``softmax_readout``, ``softmax_readout_mse`` and ``SoftmaxReadoutMSE``.
+"""The package's public functions, with the reference's signatures and errors (swvr/api.py:1-93).
 
-Same contract as the reference's swvr/api.py:1-93 (argument shapes, dtypes of
-the outputs, ValueError on bad shapes, loss reductions, module wrapper); the
-work runs in the gfx950 HIP kernels behind ``swvr::chunked_fwd`` /
-``swvr::chunked_bwd``.
+Callers see the same argument shapes, output dtypes, ValueError messages, loss
+reductions and module wrapper as the reference; underneath, every call goes to
+the gfx950 HIP library through the ``swvr::chunked_fwd`` / ``swvr::chunked_bwd``
+custom ops (and ``swvr::mse_loss`` for the loss when it applies).
 """
 import os
 
@@ -14,20 +14,23 @@ from ._ops import DEFAULT_CHUNK, REDUCTIONS, mse_loss_op, softmax_readout_op
 
 
 def default_chunk_size():
-    """Vocabulary staging chunk of the backward: env ``SWVR_CHUNK`` or 8192 (swvr/chunked.py:57-59)."""
+    """Vocabulary rows staged per step of the backward: ``SWVR_CHUNK`` if set, else 8192
+    (swvr/chunked.py:57-59)."""
     raw = os.environ.get("SWVR_CHUNK")
     return int(raw) if raw else DEFAULT_CHUNK
 
 
 def _compute_dtype(h, W):
-    """Autocast dtype when autocast is on, else the promoted input dtype (swvr/api.py:8-11)."""
+    """dtype the products run in: autocast's if it is active on h's device, otherwise the type
+    promotion of h and W (swvr/api.py:8-11)."""
     if h.device.type in ("cuda", "cpu") and torch.is_autocast_enabled(h.device.type):
         return torch.get_autocast_dtype(h.device.type)
     return torch.promote_types(h.dtype, W.dtype)
 
 
 def _check(h, W, E, bias):
-    """Shape validation with the reference's messages (swvr/api.py:14-22)."""
+    """Raise ValueError for inconsistent shapes; the messages are the reference's, word for word,
+    since callers may match on them (swvr/api.py:14-22)."""
     if W.dim() != 2 or E.dim() != 2:
         raise ValueError(f"W and E must be 2-D, got {tuple(W.shape)} and {tuple(E.shape)}")
     if h.shape[-1] != W.shape[1]:
@@ -39,13 +42,16 @@ def _check(h, W, E, bias):
 
 
 def softmax_readout(h, W, E, bias=None, *, logit_scale=1.0, chunk_size=None):
-    """Return ``(O, LSE)`` for ``S = logit_scale * h @ W.T + bias`` (swvr/api.py:25-41).
+    """Softmax-weighted readout of the embedding table (swvr/api.py:25-41).
 
-    ``O = softmax(S) @ E`` has shape ``[..., D]`` and ``LSE = logsumexp(S)`` has shape
-    ``[...]``, both fp32.  ``h`` is ``[..., K]``, ``W`` is ``[V, K]``, ``E`` is ``[V, D]`` and
-    ``bias`` is ``[V]``.  Gradients flow to every input that requires them.  The scores are
-    never materialised; the backward stages ``chunk_size`` (default 8192, or env
-    ``SWVR_CHUNK``) vocabulary rows of dS at a time, so its extra memory is O(N * chunk_size).
+    With scores ``S = logit_scale * h W^T + bias`` over the V vocabulary rows, returns the
+    probability-weighted mix of E's rows, ``O = softmax(S) E`` (shape ``h.shape[:-1] + (D,)``),
+    and the log-normaliser ``LSE = logsumexp(S)`` (shape ``h.shape[:-1]``).  Inputs:
+    h ``[..., K]``, W ``[V, K]``, E ``[V, D]``, optional bias ``[V]``.  O and LSE are fp32,
+    or fp64 when the products run in fp64.  The [tokens, V] scores never exist in memory;
+    the backward recomputes them ``chunk_size`` rows of the vocabulary at a time (default
+    8192, or ``SWVR_CHUNK``), which bounds its extra memory by O(tokens * chunk_size).
+    Autograd reaches every input that requires a gradient.
     """
     _check(h, W, E, bias)
     lead = h.shape[:-1]
@@ -59,12 +65,13 @@ def softmax_readout(h, W, E, bias=None, *, logit_scale=1.0, chunk_size=None):
 
 def softmax_readout_mse(h, W, E, target, bias=None, *, weight=None, reduction="mean",
                         z_loss_weight=0.0, logit_scale=1.0, chunk_size=None):
-    """MSE between ``softmax(S) @ E`` and ``target`` plus an optional z-loss (swvr/api.py:44-66).
+    """Squared-error loss of the readout against ``target`` (``[..., D]``) (swvr/api.py:44-66).
 
-    The per-token loss is ``mean_d (O - target)^2 + z_loss_weight * LSE^2``.  ``weight``
-    (shape ``[...]``) scales each token's loss and 0 masks it out.  ``reduction="mean"``
-    divides by ``weight.sum()`` when a weight is given, else by the token count; ``"sum"`` and
-    ``"none"`` are also accepted.
+    Each token contributes the mean over D of ``(O - target)^2``, plus ``z_loss_weight``
+    times ``LSE^2`` to keep the log-normaliser small.  An optional per-token ``weight``
+    multiplies each contribution (a zero drops the token).  ``reduction``: "mean" (the
+    weighted sum over the sum of the weights, or over the token count without weights),
+    "sum", or "none" (the per-token values).
     """
     O, lse = softmax_readout(h, W, E, bias, logit_scale=logit_scale, chunk_size=chunk_size)
     return _mse_loss(O, lse, target, weight, reduction, z_loss_weight)
@@ -100,6 +107,8 @@ def _fusable_loss(O, lse, target, weight, reduction):
     composite formula, which keeps the reference's semantics and errors."""
     if reduction not in REDUCTIONS or O.device.type != "cuda" or O.shape[-1] < 1 or lse.numel() == 0:
         return False
+    if O.dtype != torch.float32 or lse.dtype != torch.float32:  # the loss kernels read fp32 (fp64 readouts: composite)
+        return False
     if not isinstance(target, torch.Tensor) or target.shape != O.shape or target.device != O.device:
         return False
     if target.requires_grad or target.is_complex():
@@ -117,12 +126,13 @@ def _weight_of(x):
 
 
 class SoftmaxReadoutMSE(nn.Module):
-    """Loss module over an existing LM head and embedding table, without copying them
+    """``softmax_readout_mse`` as a module that refers to a model's own head and embedding
     (swvr/api.py:73-93).
 
-    ``head`` is an ``nn.Linear(K, V)`` (its bias is used if present) or a ``[V, K]`` tensor;
-    ``embedding`` is an ``nn.Embedding(V, D)`` or a ``[V, D]`` tensor.  Passing the model's own
-    modules keeps weight tying and optimizer state intact.
+    ``head``: an ``nn.Linear(K, V)``, whose bias joins the scores when it has one, or a plain
+    ``[V, K]`` tensor.  ``embedding``: an ``nn.Embedding(V, D)`` or a ``[V, D]`` tensor.  The
+    parameters are read at each call, never copied, so tied weights stay tied and optimizers
+    see the gradients on the model's tensors.
     """
 
     def __init__(self, head, embedding, *, z_loss_weight=0.0, logit_scale=1.0,

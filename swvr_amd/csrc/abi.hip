@@ -61,7 +61,7 @@ hipEvent_t take_event() {
 const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
                                      "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel",
-                                     "mse_loss",          "quantize_e4m3"};
+                                     "mse_loss",          "quantize_e4m3",      "readout_f64"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 
@@ -433,6 +433,112 @@ int swvr_fwd_fp8(int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int6
   hipError_t e = fwd_launch(kFwdFP8, plan, p, static_cast<char*>(workspace), O, lse, nullptr, nullptr,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "forward launch");
+  return SWVR_OK;
+}
+
+static int check_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, int64_t ldh, const double* W,
+                     int64_t ldw, const double* E, int64_t lde, int64_t chunk) {
+  if (N < 0 || K < 0 || V < 0 || D < 0) return fail(SWVR_EINVAL, "negative size N=%lld K=%lld V=%lld D=%lld",
+                                                    (long long)N, (long long)K, (long long)V, (long long)D);
+  if (N > INT32_MAX || K > INT32_MAX || V > INT32_MAX || D > SWVR_MAX_D)
+    return fail(SWVR_EINVAL, "sizes must fit in 32 bits and D in SWVR_MAX_D");
+  if (K >= ((int64_t)1 << 22)) return fail(SWVR_EINVAL, "K=%lld must be below 2^22", (long long)K);
+  if (chunk <= 0) return fail(SWVR_EINVAL, "chunk must be positive, got %lld", (long long)chunk);
+  if (ldh < K || ldw < K || lde < D) return fail(SWVR_EINVAL, "ldh, ldw must be >= K and lde >= D");
+  if (N > 0 && K > 0 && !h) return fail(SWVR_EINVAL, "h must be non-null");
+  if (V > 0 && K > 0 && !W) return fail(SWVR_EINVAL, "W must be non-null");
+  if (V > 0 && D > 0 && !E) return fail(SWVR_EINVAL, "E must be non-null");
+  return SWVR_OK;
+}
+
+size_t swvr_fwd_f64_workspace_size(int64_t N, int64_t V, int64_t D, int64_t chunk) {
+  if (N < 0 || V < 0 || D < 0 || chunk <= 0) return 0;
+  int64_t C;
+  size_t fb;
+  swvr::f64_plan(N, V, D, chunk, &C, &fb, nullptr);
+  return fb;
+}
+
+int swvr_fwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, int64_t ldh, const double* W,
+                 int64_t ldw, const double* E, int64_t lde, const double* bias, double logit_scale, int64_t chunk,
+                 double* O, double* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_f64(N, K, V, D, h, ldh, W, ldw, E, lde, chunk);
+  if (rc != SWVR_OK) return rc;
+  if (N == 0) return SWVR_OK;
+  if (!lse || (D > 0 && !O)) return fail(SWVR_EINVAL, "O and lse must be non-null");
+  const size_t need = swvr_fwd_f64_workspace_size(N, V, D, chunk);
+  if (!workspace || workspace_bytes < need)
+    return fail(SWVR_EWORKSPACE, "fp64 forward workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  swvr::F64Params p{};
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  p.chunk = chunk;
+  p.O = O;
+  p.lse = lse;
+  p.ws = static_cast<char*>(workspace);
+  hipError_t e = swvr::f64_fwd(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fp64 forward launch");
+  return SWVR_OK;
+}
+
+size_t swvr_bwd_f64_workspace_size(int64_t N, int64_t V, int64_t D, int64_t chunk) {
+  if (N < 0 || V < 0 || D < 0 || chunk <= 0) return 0;
+  int64_t C;
+  size_t bb;
+  swvr::f64_plan(N, V, D, chunk, &C, nullptr, &bb);
+  return bb;
+}
+
+int swvr_bwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, int64_t ldh, const double* W,
+                 int64_t ldw, const double* E, int64_t lde, const double* bias, double logit_scale, const double* O,
+                 const double* lse, const double* gO, const double* glse, int64_t chunk, double* gh, double* gW,
+                 double* gE, double* gb, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  int rc = check_f64(N, K, V, D, h, ldh, W, ldw, E, lde, chunk);
+  if (rc != SWVR_OK) return rc;
+  if (gb && !bias) return fail(SWVR_EINVAL, "gb requested without a bias");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (N > 0 && (!lse || !glse || (D > 0 && (!O || !gO))))
+    return fail(SWVR_EINVAL, "O, lse, gO and glse must be non-null");
+  const size_t need = swvr_bwd_f64_workspace_size(N, V, D, chunk);
+  if (N > 0 && (!workspace || workspace_bytes < need))
+    return fail(SWVR_EWORKSPACE, "fp64 backward workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  swvr::F64Params p{};
+  p.h = h;
+  p.ldh = ldh;
+  p.W = W;
+  p.ldw = ldw;
+  p.E = E;
+  p.lde = lde;
+  p.bias = bias;
+  p.scale = logit_scale;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.V = (int)V;
+  p.D = (int)D;
+  p.chunk = chunk;
+  p.O = const_cast<double*>(O);
+  p.lse = const_cast<double*>(lse);
+  p.gO = gO;
+  p.glse = glse;
+  p.gh = gh;
+  p.gW = gW;
+  p.gE = gE;
+  p.gb = gb;
+  p.ws = static_cast<char*>(workspace);
+  hipError_t e = swvr::f64_bwd(p, s);
+  if (e != hipSuccess) return hip_fail(e, "fp64 backward launch");
   return SWVR_OK;
 }
 

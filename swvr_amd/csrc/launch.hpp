@@ -19,6 +19,7 @@ enum KernelKind {
   kKindBwdExpand,
   kKindLoss,
   kKindQuant,
+  kKindF64,
   kNumKinds
 };
 
@@ -179,6 +180,33 @@ struct QuantParams {
   float* amax;     // per-tensor: [R] row amaxes (workspace)
 };
 hipError_t quant_launch(const QuantParams& q, hipStream_t stream);
+
+// ---------------------------------------------------------------- fp64
+struct F64Params {
+  const double* h;
+  int64_t ldh;
+  const double* W;
+  int64_t ldw;
+  const double* E;
+  int64_t lde;
+  const double* bias;  // [V] or null
+  double scale;
+  int N, K, V, D;
+  int64_t chunk;
+  double* O;            // forward: [N][D]; backward: the forward's O (read)
+  double* lse;          // forward: [N]; backward: the forward's lse (read)
+  const double* gO;     // backward: [N][D]
+  const double* glse;   // backward: [N]
+  double* gh;           // [N][K] or null
+  double* gW;           // [V][K] or null
+  double* gE;           // [V][D] or null
+  double* gb;           // [V] or null
+  char* ws;
+};
+// Vocabulary rows per chunk and workspace bytes of the fp64 forward / backward.
+void f64_plan(int64_t N, int64_t V, int64_t D, int64_t chunk, int64_t* C, size_t* fwd_bytes, size_t* bwd_bytes);
+hipError_t f64_fwd(const F64Params& p, hipStream_t stream);
+hipError_t f64_bwd(const F64Params& p, hipStream_t stream);
 hipError_t mse_launch(const MseParams& p, void* ws, hipStream_t stream);
 
 }  // namespace swvr

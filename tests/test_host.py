@@ -178,6 +178,13 @@ def test_meta_tensors_trace_through_the_fake_kernels():
     assert grads[0].dtype == torch.bfloat16
 
 
+def test_fp64_inputs_trace_to_fp64_outputs():
+    """fp64 compute returns fp64 O and lse (swvr/chunked.py:26-27), in the fakes too."""
+    h, W, E, b = (x.double() for x in make(device="meta"))
+    O, lse = swvr_amd.softmax_readout(h, W, E, b)
+    assert O.dtype == torch.float64 and lse.dtype == torch.float64
+
+
 @pytest.mark.parametrize("use_triton", [True, False])
 def test_op_schemas_take_the_reference_argument_lists(use_triton):
     """swvr::chunked_fwd / chunked_bwd with the reference's positional and keyword arguments
