@@ -4,6 +4,7 @@
     python bench.py --config 2 --steps 20 --warmup 3
     python bench.py --no-cpu             # skip the CPU baseline leg
     python bench.py --copy-probe-mib 1024  # only a plain device copy (HBM counter calibration)
+    python bench.py --mfma-probe         # only the matrix-core probe (the power / clock ceiling)
 
 A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
@@ -101,22 +102,123 @@ def kernel_flops(name, N, K, V, D, n_act=None, de_in_gemm=False):
     return 0.0
 
 
-def measured_traffic(config, kernel):
-    """Calibrated HBM bytes per launch of ``kernel`` from the committed counter summary
-    (profiles/readout_traffic.json), or None when it holds no entry for this workload."""
-    path = os.path.join(ROOT, "profiles", "readout_traffic.json")
+TRAFFIC_PATH = os.path.join(ROOT, "profiles", "readout_traffic.json")
+STREAMING_KERNELS = ("fwd_tile_kernel", "bwd_scores_kernel", "bwd_gemm_kernel")
+
+
+def source_sha():
+    """SHA-256 (16 hex digits) of the HIP sources the library is built from: counter figures
+    measured on another build of them are stale."""
+    import hashlib
+    d = os.path.join(ROOT, "swvr_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".hpp")):
+            h.update(name.encode())
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def load_traffic():
+    """The committed counter summary (profiles/readout_traffic.json) and whether it was measured
+    on these sources."""
     try:
-        with open(path) as f:
+        with open(TRAFFIC_PATH) as f:
             t = json.load(f)
+    except (OSError, ValueError):
+        return None, False
+    return t, t.get("source_sha") == source_sha()
+
+
+def measured_traffic(t, config, kernel):
+    """Calibrated HBM (fetch, write) bytes per launch of ``kernel`` at ``config``, or None."""
+    try:
         e = t["configs"][str(config)][kernel]
-    except (OSError, KeyError, ValueError):
+    except (TypeError, KeyError):
         return None
-    return int(e["fetch_kib"] * 1024 * t["fetch_scale"] + e["write_kib"] * 1024 * t["write_scale"])
+    return e["fetch_kib"] * 1024 * t["fetch_scale"], e["write_kib"] * 1024 * t["write_scale"]
+
+
+def algorithmic_bytes(name, N, K, V, D, chunk, n_act, wide):
+    """Bytes one launch must move at least: each operand read once, each result written once.
+    fwd: h, W, E in, O and lse out.  scores (a chunk of C rows): h of the active tokens, W_c, E_c,
+    gO in; the dS stage (and the P stage of the wide kernel) out.  gradient GEMM (a chunk): the dS
+    stage, h, W_c in; gW_c out; the fp32 dh accumulator read and written."""
+    C = min(chunk, V)
+    if name == "fwd_tile_kernel":
+        return 2 * (N * K + V * K + V * D) + 4 * N * (D + 1)
+    if name == "bwd_scores_kernel":
+        return 2 * (n_act * K + C * K + C * D + n_act * D) + 2 * C * n_act * (2 if wide else 1)
+    if name == "bwd_gemm_kernel":
+        return 2 * (C * n_act + n_act * K + 2 * C * K) + 8 * n_act * K + (2 * C * n_act if wide else 0)
+    return None
+
+
+def traffic_summary(root):
+    """The traffic file from rocprofv3 counter runs under ``root``: fetch_c<N>/ and write_c<N>/
+    (FETCH_SIZE and WRITE_SIZE passes of ``bench.py --config N --no-cpu --no-fp8``) and copy_fetch/,
+    copy_write/ (the same counters over ``bench.py --copy-probe-mib 1024``, which moves 1 GiB each
+    way per launch and calibrates them).  Per-dispatch averages of this package's streaming kernels."""
+    import csv
+    import glob
+    import re
+
+    def per_kernel(d, counter):
+        acc = {}
+        for f in glob.glob(os.path.join(root, d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                m = re.search(r"(fwd_tile_kernel|bwd_scores_ring_kernel|bwd_scores_wide_kernel|bwd_scores_kernel|"
+                              r"bwd_gemm_kernel|elementwise_kernel|copy)", r["Kernel_Name"])
+                if not m:
+                    continue
+                k = "bwd_scores_kernel" if m.group(1).startswith("bwd_scores") else m.group(1)
+                acc.setdefault(k, []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}, {k: len(v) for k, v in acc.items()}
+
+    mib = 1024 * 1024
+    cf, _ = per_kernel("copy_fetch", "FETCH_SIZE")
+    cw, _ = per_kernel("copy_write", "WRITE_SIZE")
+    copy_f = max(cf.values()) if cf else None
+    copy_w = max(cw.values()) if cw else None
+    out = {"about": "HBM bytes per dispatch of the streaming kernels: rocprofv3 FETCH_SIZE and WRITE_SIZE (KiB per "
+                    "dispatch, averaged) scaled by what the same counters read for a plain 1 GiB copy; "
+                    "bytes = fetch_kib * 1024 * fetch_scale + write_kib * 1024 * write_scale. "
+                    "source_sha: the HIP sources measured (bench.py source_sha).",
+           "source_sha": source_sha(),
+           "fetch_scale": round(mib / copy_f, 4) if copy_f else None,
+           "write_scale": round(mib / copy_w, 4) if copy_w else None,
+           "copy_probe_kib": {"fetch": copy_f, "write": copy_w},
+           "configs": {}}
+    for c in sorted(CONFIGS):
+        f, nf = per_kernel(f"fetch_c{c}", "FETCH_SIZE")
+        w, _ = per_kernel(f"write_c{c}", "WRITE_SIZE")
+        if f:
+            out["configs"][str(c)] = {k: {"fetch_kib": round(f[k], 1), "write_kib": round(w.get(k, 0.0), 1),
+                                          "dispatches": nf[k]} for k in STREAMING_KERNELS if k in f}
+    return out
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg, tokens, chunk, device):
-    """Time oracle/chunked.py (the reference's CPU algorithm) fwd+bwd on `tokens` tokens."""
+    """Time oracle/chunked.py (the reference's CPU algorithm) fwd+bwd on `tokens` tokens, on every
+    host CPU this process may use (the affinity mask, capped by OMP_NUM_THREADS when it is set)."""
     from oracle import chunked
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    torch.set_num_threads(min(usable, cap) if cap > 0 else usable)
     N, K, V, D = cfg["N"], cfg["K"], cfg["V"], cfg["D"]
     g = torch.Generator(device=device).manual_seed(1)
     r = lambda *s, sc=1.0: (sc * torch.randn(*s, device=device, generator=g)).to(torch.bfloat16).cpu()
@@ -131,8 +233,11 @@ def cpu_baseline(cfg, tokens, chunk, device):
     dt = time.perf_counter() - t0
     _, flops = algorithmic_flops(tokens, K, V, D)
     return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "os_cpu_count": os.cpu_count(), "usable_cpus": usable, "torch_threads": threads,
+            "cpu_model": cpu_model(), "seconds": round(dt, 2),
             "sample": f"fwd+bwd of {tokens} tokens x the full V={V}, K={K}, D={D} (bf16 operands upcast "
-                      f"to fp32 BLAS, vocabulary chunk {chunk}) in {dt:.1f} s on {threads} threads"}
+                      f"to fp32 BLAS, vocabulary chunk {chunk}) in {dt:.1f} s on {threads} threads; the "
+                      f"rate is the workload's 2 N V (4K + 3D) flops over that time (one timed iteration)"}
 
 
 def copy_probe(mib):
@@ -143,6 +248,33 @@ def copy_probe(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_mib": mib, "launches": 5}), flush=True)
+
+
+def mfma_probe(iters=1 << 20, launches=3):
+    """Matrix-core rate of the bare k16 step (swvr_probe_mfma): 256 workgroups of 8 waves (one per
+    CU, two waves per SIMD, as the hot kernels), each wave-step 8 x 32x32x16 bf16 MFMAs = 2^18 flops.
+    Modes: random operands in registers, zeros in registers, random operands read from LDS each
+    step.  The launches of a mode run back to back; the rate is the mean over them."""
+    from swvr_amd import _lib
+    lib = _lib.load()
+    wgs = 256
+    out = torch.empty(wgs * 512, dtype=torch.float32, device="cuda")
+    flops = float(wgs) * 8 * iters * 2.0 ** 18
+    res = {}
+    for mode, name in ((0, "random_registers"), (1, "zero_registers"), (2, "random_lds")):
+        _lib.check(lib.swvr_probe_mfma(wgs, 1 << 14, mode, _lib.ptr(out), _lib.stream_of(out.device)))
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(launches):
+            _lib.check(lib.swvr_probe_mfma(wgs, iters, mode, _lib.ptr(out), _lib.stream_of(out.device)))
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / launches
+        tf = flops / (ms * 1e-3) / 1e12
+        res[name] = {"ms_per_launch": round(ms, 2), "tflops": round(tf, 1), "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1)}
+        print(json.dumps({"mfma_probe": name, **res[name]}), flush=True)
+    return res
 
 
 def fp8_path(h, W, E, b, target, weight, z, chunk, params, fwd_flops, flops, iters):
@@ -209,9 +341,22 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device-to-device copy of this many MiB, 5 times, and exit: "
                          "its FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc calibrate the HBM traffic counters")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the opt-in e4m3 leg")
+    ap.add_argument("--traffic-from", default=None,
+                    help="print the traffic summary (profiles/readout_traffic.json) built from rocprofv3 "
+                         "counter runs under this directory, and exit")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="run only the matrix-core probe (swvr_probe_mfma: the bare MFMA step with random, zero "
+                         "and LDS-fed operands) and print its rates")
     args = ap.parse_args()
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.mfma_probe:
+        print(json.dumps({"mfma_probe_summary": mfma_probe()}), flush=True)
+        return
+    if args.traffic_from:
+        print(json.dumps(traffic_summary(args.traffic_from), indent=1))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only (N=1); multi-GPU runs are not part of it"}))
@@ -272,23 +417,36 @@ def main():
     fwd_flops, flops = algorithmic_flops(N, K, V, D)
     tflops = flops / (ms * 1e-3) / 1e12
     fp8 = (fp8_path(h, W, E, b, target, weight, cfg["z"], args.chunk, params, fwd_flops, flops, fwd_iters)
-           if D <= 128 else None)
+           if D <= 128 and not args.no_fp8 else None)
     # tokens with a non-zero weight: the others have zero cotangents, and the
     # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
     n_act = int((weight != 0).sum().item()) if weight is not None else N
     de_in_gemm = _lib.bwd_tiling(torch.bfloat16, N, K, V, D, args.chunk)["kernel"] == 2
+    traffic, fresh = load_traffic()
     per_kernel = {}
+    stream_bytes = stream_ms = 0.0
     for name, (kms, cnt) in kernels.items():
         kf = kernel_flops(name, N, K, V, D, n_act, de_in_gemm) * args.steps
         per_kernel[name] = {"ms_per_step": round(kms / args.steps, 3), "launches_per_step": cnt // args.steps,
                             "avg_launch_ms": round(kms / cnt, 4),
                             "tflops": round(kf / (kms * 1e-3) / 1e12, 1) if kf else None}
+        alg = algorithmic_bytes(name, N, K, V, D, args.chunk, n_act, de_in_gemm)
+        tr = measured_traffic(traffic, args.config, name) if fresh else None
+        if alg is not None:
+            per_kernel[name]["algorithmic_bytes_per_launch"] = int(alg)
+        if tr is not None:
+            per_kernel[name]["hbm_fetch_bytes_per_launch"] = int(tr[0])
+            per_kernel[name]["hbm_write_bytes_per_launch"] = int(tr[1])
+            per_kernel[name]["fetch_over_algorithmic"] = round(tr[0] / alg, 2) if alg else None
+            stream_bytes += (tr[0] + tr[1]) * cnt
+            stream_ms += kms
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     dk = per_kernel[dom]
     launch_flops = kernel_flops(dom, N, K, V, D, n_act, de_in_gemm) / dk["launches_per_step"]
     achieved = launch_flops / (dk["avg_launch_ms"] * 1e-3) / 1e12
     # W and E bytes the algorithm streams per step: fwd (W, E), bwd scores (W, E), dh GEMM (W)
     we_bytes = (3 * V * K + 2 * V * D) * 2
+    dom_tr = measured_traffic(traffic, args.config, dom) if fresh else None
 
     out = {
         "metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1,
@@ -304,11 +462,17 @@ def main():
         "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
         "peak_gib": round(peak_gib, 3),
-        "we_stream_gbps": round(we_bytes / (ms * 1e-3) / 1e9, 1),
+        # HBM rate of the kernels that stream W and E: their counter-measured bytes (FETCH_SIZE +
+        # WRITE_SIZE, calibrated, profiles/readout_traffic.json) over their own time; null when the
+        # counters were taken on other sources
+        "we_stream_gbps": round(stream_bytes / (stream_ms * 1e-3) / 1e9, 1) if stream_ms else None,
+        "we_algorithmic_gbps": round(we_bytes / (ms * 1e-3) / 1e9, 1),
+        "traffic_source": {"file": "profiles/readout_traffic.json", "source_sha": source_sha(),
+                           "measured_sha": traffic.get("source_sha") if traffic else None, "fresh": fresh},
         "kernels": per_kernel,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic(args.config, dom)},
+                     "traffic": int(dom_tr[0] + dom_tr[1]) if dom_tr else None},
         "fp8": fp8,
         "published_reference_ms": {"A100": {3: 240, 2: 115, 4: 160}.get(args.config),
                                    "H200": {3: 98, 2: 48, 4: 62}.get(args.config)},

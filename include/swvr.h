@@ -265,6 +265,15 @@ int swvr_mse_loss_noalloc(int64_t N, int64_t D, const float* O, const float* lse
                           int target_dtype, int64_t ldt, const float* weight, float z_loss_weight, int reduction,
                           float* out, float* scale, float* gO, float* glse, void* stream);
 
+/* Matrix-core throughput probe (measurement only; no reference counterpart):
+ * `workgroups` workgroups of 8 waves, each wave `iters` steps of a 4 x 2 grid
+ * of 32x32x16 bf16 MFMAs (2^18 flops per wave-step) on operands from
+ * mode 0: random values in registers, 1: zeros in registers, 2: random values
+ * read from LDS every step (6 x 16 bytes per lane per 8 MFMAs, the hot loops'
+ * pattern).  out receives workgroups * 512 floats (the accumulator sums).
+ * Timed, it measures the rate the chip sustains for such data. */
+int swvr_probe_mfma(int64_t workgroups, int64_t iters, int mode, float* out, void* stream);
+
 /* Instrumentation (no reference counterpart).  While enabled, every kernel
  * launch is bracketed by a pair of HIP events on its stream.
  * swvr_timing_collect synchronises those events, writes per-kernel-kind total

@@ -55,6 +55,7 @@ SIGNATURES = {
     "swvr_mse_loss_workspace_size": (_sz, [_i64]),
     "swvr_mse_loss": (_i, [_i64, _i64, _p, _p, _p, _i, _i64, _p, _f, _i, _p, _p, _p, _p, _p, _sz, _p]),
     "swvr_mse_loss_noalloc": (_i, [_i64, _i64, _p, _p, _p, _i, _i64, _p, _f, _i, _p, _p, _p, _p, _p]),
+    "swvr_probe_mfma": (_i, [_i64, _i64, _i, _p, _p]),
     "swvr_timing_enable": (_i, [_i]),
     "swvr_timing_collect": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _i]),
     "swvr_kernel_name": (ctypes.c_char_p, [_i]),
@@ -122,7 +123,7 @@ def kernel_timing(enable=None):
     if enable is not None:
         lib.swvr_timing_enable(1 if enable else 0)
         return None
-    n = 16
+    n = 32
     ms = (ctypes.c_double * n)()
     cnt = (ctypes.c_int64 * n)()
     k = lib.swvr_timing_collect(ms, cnt, n)

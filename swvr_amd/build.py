@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libswvr_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["fwd.hip", "bwd.hip", "loss.hip", "quant.hip", "f64.hip", "abi.hip"]
+SOURCES = ["fwd.hip", "bwd.hip", "loss.hip", "quant.hip", "f64.hip", "probe.hip", "abi.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are kept out of the code objects; the host pass warns

@@ -61,7 +61,8 @@ hipEvent_t take_event() {
 const char* kKindNames[kNumKinds] = {"fwd_tile_kernel",   "fwd_combine_kernel", "bwd_pack_kernel",
                                      "bwd_scores_kernel", "bwd_gemm_kernel",    "bwd_reduce_kernel",
                                      "fill_zero_kernel",  "operand_packing",    "bwd_expand_kernel",
-                                     "mse_loss",          "quantize_e4m3",      "readout_f64"};
+                                     "mse_loss",          "quantize_e4m3",      "readout_f64",
+                                     "probe_mfma"};
 
 bool is_dtype(int d) { return d == SWVR_BF16 || d == SWVR_F16 || d == SWVR_F32; }
 
@@ -539,6 +540,16 @@ int swvr_bwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, in
   p.ws = static_cast<char*>(workspace);
   hipError_t e = swvr::f64_bwd(p, s);
   if (e != hipSuccess) return hip_fail(e, "fp64 backward launch");
+  return SWVR_OK;
+}
+
+int swvr_probe_mfma(int64_t workgroups, int64_t iters, int mode, float* out, void* stream) {
+  g_err[0] = 0;
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 24) || mode < 0 || mode > 2)
+    return fail(SWVR_EINVAL, "probe: workgroups in [1, 2^20], iters in [1, 2^24], mode 0, 1 or 2");
+  if (!out) return fail(SWVR_EINVAL, "out must be non-null");
+  hipError_t e = swvr::probe_mfma((int)workgroups, (int)iters, mode, out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "probe launch");
   return SWVR_OK;
 }
 

@@ -20,6 +20,7 @@ enum KernelKind {
   kKindLoss,
   kKindQuant,
   kKindF64,
+  kKindProbe,
   kNumKinds
 };
 
@@ -207,6 +208,10 @@ struct F64Params {
 void f64_plan(int64_t N, int64_t V, int64_t D, int64_t chunk, int64_t* C, size_t* fwd_bytes, size_t* bwd_bytes);
 hipError_t f64_fwd(const F64Params& p, hipStream_t stream);
 hipError_t f64_bwd(const F64Params& p, hipStream_t stream);
+
+// Matrix-core throughput probe (probe.hip): workgroups of 8 waves, iters k16 steps of
+// 8 MFMAs per wave; out receives workgroups * 512 floats.
+hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream_t stream);
 hipError_t mse_launch(const MseParams& p, void* ws, hipStream_t stream);
 
 }  // namespace swvr
