@@ -7,7 +7,9 @@
 //   0  random bf16 operands held in registers (values spread like N(0,1) data);
 //   1  zero operands in registers (the same instructions at the lowest power);
 //   2  random operands read from LDS every step, 6 x 16-byte reads per 8
-//      MFMAs, as the forward / gradient GEMM loops read them.
+//      MFMAs, as the forward / gradient GEMM loops read them;
+//   3, 4  the same with 4 and 3 reads per 8 MFMAs (the read rate of larger
+//      wave tiles), which shows how much the LDS read rate costs.
 // Comparing the rates shows how much of the datasheet peak this chip reaches
 // with the operand data and LDS traffic of the real kernels, i.e. the ceiling
 // that power and clock set for them.
@@ -59,14 +61,19 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, int mode, ui
   const char* lb = reinterpret_cast<const char*>(lds);
   const int wb = wave_id() * 1024;
   for (int it = 0; it < iters; ++it) {
-    if (mode == 2) {
-      // six 16-byte operand reads per step, one 1 KB wave-wide piece each, from the
-      // 8 KB window (it % 4) of the 32 KB: offsets stay below 4 * 8192
+    if (mode >= 2) {
+      // 16-byte operand reads per step, one 1 KB wave-wide piece each, from the
+      // 8 KB window (it % 4) of the 32 KB: offsets stay below 4 * 8192.  mode 2 reads
+      // all six operands (a 128 x 64 wave tile), 3 four (the operand count per MFMA of
+      // a 128 x 128 tile), 4 three
       const char* win = lb + (it & 3) * 8192 + lane * 16;
+      const int na = mode == 2 ? 4 : mode == 3 ? 3 : 2;
 #pragma unroll
-      for (int f = 0; f < 4; ++f) a[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + f * 1024) & 8191));
+      for (int f = 0; f < 4; ++f)
+        if (f < na) a[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + f * 1024) & 8191));
 #pragma unroll
-      for (int f = 0; f < 2; ++f) b[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
+      for (int f = 0; f < 2; ++f)
+        if (mode == 2 || f == 0) b[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
