@@ -34,9 +34,11 @@ template <class T, int DP>
 struct FwdTile {
   static constexpr bool wide = sizeof(T) == 2;
   static constexpr bool narrow = wide && DP <= 64;
-  // 2-byte dtypes: 128 x 64 waves (D <= 64), 64 x 64 (D = 128), 64 x 32 (D = 256): the widest
-  // whose score and acc^T accumulators fit beside the operands
-  static constexpr int BV = wide ? (DP <= 128 ? 256 : 128) : 128;
+  // D = 256 (2-byte dtypes): E^T streamed through the ring in D-slices (fwd_stream_kernel)
+  static constexpr bool stream_e = wide && DP == 256;
+  // 2-byte dtypes: 128 x 64 waves (D <= 64), 64 x 64 (D = 128), 128 x 32 (D = 256, E^T streamed):
+  // the widest whose score and acc^T accumulators fit beside the operands
+  static constexpr int BV = wide ? 256 : 128;
   static constexpr int BM = narrow ? 256 : wide ? 128 : 64;
   static constexpr int WV = narrow ? 2 : wide ? (DP == 128 ? 4 : 2) : 2;
   static constexpr int WT = narrow ? 4 : wide ? (DP == 128 ? 2 : 4) : 2;
@@ -306,6 +308,207 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
   }
 }
 
+// Forward for D = 256 (2-byte dtypes): E^T is not pinned in LDS.  Per
+// vocabulary tile the ring carries the nk K-slices of W and h (-> S^T), then
+// the 8 D-slices of the tile's packed E^T (32 x BV each, 16 KB, one stage
+// slot each), so the LDS holds only the ring: 256 vocabulary rows x 128
+// tokens per workgroup of 8 waves (2 vocabulary halves x 4 token quarters,
+// 128 x 32 each), twice the tile the pinned 64 KB E^T tile left room for
+// (85 flop per byte of operand traffic instead of 64).  The bias of a tile
+// is loaded with its first K-slice into a double-buffered strip.
+template <class T, int DP>
+__global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdParams p) {
+  typedef FwdTile<T, DP> C;
+  typedef typename Vec8<T>::type V8;
+  constexpr int kBK = SliceK<T>::value;
+  constexpr int BV = C::BV, BM = C::BM, NT = C::NT, NS = C::NS;
+  constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
+  typedef PackedKLoader<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile (packed)
+  typedef PackedKLoader<T, BM, kBK, NT> TB;  // h rows of the token block (packed)
+  constexpr int DS = 32;                     // E^T rows (embedding columns) per D-slice
+  typedef KTile<T, DS, BV, NT> TE;           // one D-slice of the packed E^T tile, pe_row order
+  constexpr int SB = TA::BYTES + TB::BYTES;
+  constexpr int L = TA::NI + TB::NI;         // loads per thread per stage (E stages padded to it)
+  static_assert(sizeof(T) == 2 && DP % DS == 0 && TE::BYTES <= SB && TE::NI <= L, "E^T slices fit a stage");
+  static_assert(!TA::PARTIAL && !TB::PARTIAL && !TE::PARTIAL, "whole loads");
+  constexpr int FV = WVR / 32, FT = WTR / 32;  // 32x32 blocks per wave
+  constexpr int DB = DP / 32, ND = DP / DS;
+
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * BV * 4];
+  const float* const sBias = reinterpret_cast<const float*>(smem + NS * SB);  // [2][BV]
+
+  const int lane = lane_id(), w = wave_id();
+  const int wv = w / C::WT, wt = w % C::WT;
+  int split, tb;
+  grouped_tile(blockIdx.x, p.n_split, p.n_tb, &split, &tb);
+  const int n0 = tb * BM;
+  const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
+  const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
+  const T* Ep = static_cast<const T*>(p.Ep);
+
+  float m[FT], l[FT];
+  f32x16_t oacc[DB][FT];
+#pragma unroll
+  for (int ft = 0; ft < FT; ++ft) {
+    m[ft] = kNegInf;
+    l[ft] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db][ft] = zero16();
+  }
+
+  const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
+  const int n_tiles = vt_end - vt_begin;
+  const int per_tile = nk + ND;
+  const int total = n_tiles * per_tile;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t ldsB = lds0 + NS * SB;
+  TA ta;
+  ta.setup(p.Wp, vt_begin * BV, p.hS);
+  TB tbh;
+  tbh.setup(p.hp, n0, p.hS);
+  TE te;
+  te.setup(Ep, BV, DS, BV);
+  const rsrc_t r_none = make_rsrc(nullptr);
+  // issue cursor over the walk: stage `issued` is (tile is_tile, sub-stage
+  // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk.. the D-slices of E^T
+  int issued = 0, is_tile = 0, is_sub = 0, is_slot = 0;
+  auto issue_next = [&]() {
+    if (issued >= total) return;
+    const uint32_t st = lds0 + is_slot * SB;
+    const int v0 = (vt_begin + is_tile) * BV;
+    if (is_sub < nk) {
+      if (is_sub == 0) {
+        ta.rebase(v0);
+        // the tile's bias into strip (tile & 1), ahead of its slices (wave 0)
+        if ((int)threadIdx.x * 16 < BV * 4)
+          dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + (is_tile & 1) * (BV * 4) + w * 1024);
+      }
+      ta.issue(st, is_sub * kBK);
+      tbh.issue(st + TA::BYTES, is_sub * kBK);
+    } else {
+      // rows d0 .. d0 + 31 of the tile's E^T [DP][BV]: one contiguous run
+      te.base = reinterpret_cast<const char*>(Ep + ((int64_t)v0 * DP + (int64_t)(is_sub - nk) * DS * BV));
+      te.issue(st, 0);
+#pragma unroll
+      for (int i = TE::NI; i < L; ++i) dma_batch1(r_none, kOOB, st + i * NT * 16 + w * 1024);
+    }
+    ++issued;
+    if (++is_sub == per_tile) {
+      is_sub = 0;
+      ++is_tile;
+    }
+    is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue_next();
+
+  f32x16_t sacc[FV][FT];
+  Ring<NS> ring{NS - 1, total};  // the first publish_next() moves to stage 0, slot 0
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    // first K-slice of the tile; every wave has also finished the previous
+    // tile's E^T slices, and its bias strip is free again
+    ring.template publish_next<L>();
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
+    tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
+
+    // ---- scores -> running softmax of this wave's slice of the tile
+    const float* sB = sBias + (tile & 1) * BV + opaque_zero();
+    float mx[FT];
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft) mx[ft] = kNegInf;
+#pragma unroll
+    for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        // registers 4g..4g+3 hold rows 8g + 4(lane/32) + 0..3 of the block
+        const int row = wv * WVR + fv * 32 + 8 * g + (lane >> 5) * 4;
+        const float4 b4 = *reinterpret_cast<const float4*>(sB + row);
+        const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int ft = 0; ft < FT; ++ft) {
+            const float x = fmaf(sacc[fv][ft][4 * g + i], p.scale, bb[i]);  // rounded as the backward rounds it
+            sacc[fv][ft][4 * g + i] = x;
+            mx[ft] = fmaxf(mx[ft], x);
+          }
+      }
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft) {
+      const float mnew = fmaxf(m[ft], wave_max32(mx[ft]));
+      // a column whose scores so far are all -inf keeps m = -inf; shift it by 0
+      // (swvr/chunked.py:98-99)
+      const float shift = mnew == kNegInf ? 0.f : mnew;
+      const float alpha = fast_exp(m[ft] - shift);
+      m[ft] = mnew;
+      float rs = 0.f;
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp(sacc[fv][ft][r] - shift);
+          sacc[fv][ft][r] = pv;
+          rs += pv;
+        }
+      l[ft] = l[ft] * alpha + wave_sum32(rs);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][ft][r] *= alpha;
+    }
+
+    // ---- acc^T[d][token] += E^T[d][v] P^T[v][token], one D-slice per stage.
+    // Score registers 8c..8c+7 of a block are the B operand of one k16 step;
+    // they hold vocabulary rows 16c + 8(t/4) + 4(lane/32) + t%4, which the
+    // packed E^T stores contiguously (pe_row): one read per operand.
+#pragma unroll
+    for (int ds = 0; ds < ND; ++ds) {
+      ring.template publish_next<L>();
+      issue_next();
+      const char* sEe = smem + ring.slot * SB + opaque_zero();
+      const int d = lane & 31;
+#pragma unroll
+      for (int fv = 0; fv < FV; ++fv)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int p0 = wv * WVR + fv * 32 + 8 * (2 * c + (lane >> 5));
+          const V8 av = *reinterpret_cast<const V8*>(sEe + TE::elem(d, p0));
+#pragma unroll
+          for (int ft = 0; ft < FT; ++ft) {
+            V8 bv;
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[fv][ft][8 * c + tt]);
+            mfma_k16(oacc[ds][ft], av, bv);
+          }
+        }
+    }
+  }
+
+  // ---- partial (m, l, acc) of this wave's vocabulary slice of this split
+  const int part = split * C::WV + wv;
+  const int ln = lane + opaque_zero();
+#pragma unroll
+  for (int ft = 0; ft < FT; ++ft) {
+    const int n = n0 + wt * WTR + ft * 32 + (ln & 31);
+    if (n < p.N) {
+      if (ln < 32) {
+        p.part_m[(int64_t)part * p.N + n] = m[ft];
+        p.part_l[(int64_t)part * p.N + n] = l[ft];
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = db * 32 + c_row(r, ln);
+          p.part_acc[((int64_t)part * DP + d) * p.N + n] = oacc[db][ft][r];
+        }
+    }
+  }
+}
+
 // Merge partial softmaxes in a fixed order (O rows ldo apart): O = sum_p acc_p e^(m_p - M) /
 // sum_p l_p e^(m_p - M), LSE = M + log(...).  A row with every score -inf ends
 // with M = -inf, L = 0: O = NaN and LSE = -inf, as swvr/chunked.py:105 gives.
@@ -352,7 +555,10 @@ hipError_t launch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stre
   if (plan.BV != C::BV || plan.BM != C::BM) return hipErrorInvalidValue;
   const int blocks = plan.n_tb * plan.n_split;
   timing_begin(kKindFwdTile, stream);
-  fwd_tile_kernel<T, DP, F8><<<blocks, C::NT, 0, stream>>>(p);
+  if constexpr (!F8 && FwdTile<T, DP>::stream_e)
+    fwd_stream_kernel<T, DP><<<blocks, C::NT, 0, stream>>>(p);
+  else
+    fwd_tile_kernel<T, DP, F8><<<blocks, C::NT, 0, stream>>>(p);
   timing_end(kKindFwdTile, stream);
   return hipGetLastError();
 }

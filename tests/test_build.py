@@ -28,8 +28,8 @@ def test_no_kernel_spills_or_uses_scratch(usage):
 
 
 @pytest.mark.parametrize("kernel", ["fwd_tile_kernel<bf16,64,0>", "bwd_scores_ring_kernel<bf16,64,0>",
-                                    "bwd_gemm_kernel<bf16>", "bwd_scores_wide_kernel<bf16,256>",
-                                    "fwd_tile_kernel<bf16,256,0>"])
+                                    "bwd_gemm_kernel<bf16>", "bwd_scores_wide_kernel<bf16>",
+                                    "fwd_stream_kernel<bf16,256>"])
 def test_hot_kernels_run_two_waves_per_simd_within_lds(usage, kernel):
     """The headline tiles are 8 waves of 512 threads: two waves per SIMD, one workgroup per CU."""
     u = usage[kernel]
