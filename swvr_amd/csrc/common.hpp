@@ -162,48 +162,53 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // saved and restored around the batch).  Issued from inline assembly so that
 // the compiler does not guard every later LDS read with a wait for all
 // outstanding loads: the reduction loops order these loads themselves
-// (wait_stages + stage_barrier).
+// (wait_stages + stage_barrier).  On this chip generation an LDS-DMA load
+// that follows a scalar write of M0 needs one wait state, or it may take the
+// previous M0 and write a wrong LDS address; the compiler inserts that wait
+// for its own code but not inside assembly, hence the s_nop after each write.
+// s_add_u32 on M0 also writes SCC, so the assembly declares SCC clobbered (the
+// compiler may otherwise keep a comparison's result in SCC across the batch).
 __device__ __forceinline__ void dma_batch1(rsrc_t r, uint32_t v0, uint32_t lds_any) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_any);
   uint32_t save;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(save)
       : "v"(v0), "s"(r), "s"(lds)
-      : "memory");
+      : "memory", "scc");
 }
 template <int STEP>
 __device__ __forceinline__ void dma_batch2(rsrc_t r, uint32_t v0, uint32_t v1, uint32_t lds) {
   uint32_t save;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %4\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %4\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, %5\n\t"
+      "s_add_u32 m0, m0, %5\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(save)
       : "v"(v0), "v"(v1), "s"(r), "s"(lds), "i"(STEP)
-      : "memory");
+      : "memory", "scc");
 }
 template <int STEP>
 __device__ __forceinline__ void dma_batch4(rsrc_t r, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
                                            uint32_t lds) {
   uint32_t save;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %6\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %6\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, %7\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, %7\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %3, %5, 0 offen lds\n\t"
-      "s_add_u32 m0, m0, %7\n\t"
+      "s_add_u32 m0, m0, %7\n\ts_nop 0\n\t"
       "buffer_load_dwordx4 %4, %5, 0 offen lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(save)
       : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(r), "s"(lds), "i"(STEP)
-      : "memory");
+      : "memory", "scc");
 }
 // NI loads of one thread, STEP bytes apart in LDS starting at lds.
 template <int NI, int STEP>

@@ -256,3 +256,18 @@ def test_zero_hidden_size():
     want = torch.softmax(bd.double(), 0) @ Ed.double()
     torch.testing.assert_close(O.double(), want.expand_as(O), **TOL)
     torch.testing.assert_close(lse.double(), torch.logsumexp(bd.double(), 0).expand(N), **TOL)
+
+
+@pytest.mark.parametrize("dtype,N,K,V,D", [
+    (torch.bfloat16, 40, 32, 1000, 64), (torch.bfloat16, 300, 32, 3000, 16), (torch.float16, 40, 32, 1000, 200),
+    (torch.float32, 40, 16, 1000, 64), (torch.float32, 40, 16, 1000, 128), (torch.bfloat16, 6, 32, 300, 5),
+])
+def test_one_slice_stages_over_several_vocabulary_tiles(dtype, N, K, V, D):
+    """K of one reduction slice: every ring stage is a whole vocabulary tile, so the forward's
+    first stages are issued back to back (a stale condition code once reloaded tile 0 there)."""
+    h, W, E, b = make(N=N, K=K, V=V, D=D, dtype=dtype)
+    O, lse = swvr.softmax_readout(h, W, E, b)
+    O_r, lse_r = ref.softmax_readout_reference(*(x.detach().cpu().double() for x in (h, W, E, b)))
+    tol = 1e-5 if dtype == f32 else 1e-2
+    assert rel_err(lse, lse_r) < tol / 10
+    assert rel_err(O, O_r) < tol

@@ -118,6 +118,12 @@ CASES = [
     ("wide-f32-D200", f32, 2048 + 1, 64, 8192, 200, 8192),
     ("general-f32-D64", f32, 2048 + 9, 128, 8192, 64, 8192),
     ("general-f32-D128", f32, 2048 + 3, 64, 4096, 128, 4096),
+    # one reduction slice per stage (K = one slice): the stage cursor advances a whole
+    # token block per issue, the case a stale condition code once broke
+    ("ring-bf16-D64-K32", bf16, 8192 + 77, 32, 8192 + 300, 64, 8192),
+    ("wide-bf16-D128-K32", bf16, 4096 + 33, 32, 8192 + 128, 128, 8192),
+    ("general-f32-D64-K16", f32, 2048 + 9, 16, 8192, 64, 8192),
+    ("general-f32-D128-K16", f32, 2048 + 3, 16, 4096, 128, 4096),
 ]
 
 
