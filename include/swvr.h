@@ -93,6 +93,28 @@ int swvr_fwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    const void* E, int64_t lde, const float* bias, float logit_scale,
                    float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
+/* swvr_fwd_mixed for a weighted loss (swvr/api.py:53-66, which multiplies each
+ * token's loss by weight[n]): only the tokens with weight[n] != 0 (fp32 [N]; a
+ * NaN weight counts as non-zero) are computed; the O rows and lse of the others
+ * are written as 0.  Their loss term weight[n] * (mean_d (O - target)^2 +
+ * z * lse^2) is then 0 * finite = 0, as the reference's is, except where the
+ * reference's is 0 * NaN; those rows are computed too:
+ *   - a zero-weight token whose h row holds an infinity or a NaN;
+ *   - every token, when W, E or the bias holds a NaN or +inf, every bias entry
+ *     is -inf, V = 0, or logit_scale is not finite.
+ * (A zero-weight token whose fp32 scores overflow from finite inputs is the one
+ * case left: its reference loss is NaN, here 0 * finite.)  O and lse of the
+ * computed tokens equal swvr_fwd_mixed's to fp32 rounding (the vocabulary is
+ * split differently over the fewer tokens).  No reference counterpart: the
+ * reference computes every token's readout before weighting the loss.
+ * Workspace: swvr_fwd_active_workspace_size. */
+size_t swvr_fwd_active_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D);
+int swvr_fwd_active(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
+                    const void* h, int64_t ldh, const void* W, int64_t ldw,
+                    const void* E, int64_t lde, const float* bias, float logit_scale,
+                    const float* weight, float* O, float* lse,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Vocabulary-parallel forward, one shard.  With W, E and bias holding V rows of
  * the vocabulary (a shard), writes the shard's softmax partials, fp32:
  *   m[n]     = max_v S[n,v]

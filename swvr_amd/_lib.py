@@ -28,6 +28,9 @@ SIGNATURES = {
                       _p, _p, _p, _sz, _p]),
     "swvr_fwd_mixed": (_i, [_i, _i, _i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f,
                             _p, _p, _p, _sz, _p]),
+    "swvr_fwd_active_workspace_size": (_sz, [_i, _i64, _i64, _i64, _i64]),
+    "swvr_fwd_active": (_i, [_i, _i, _i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f,
+                             _p, _p, _p, _p, _sz, _p]),
     "swvr_bwd_workspace_size_mixed": (_sz, [_i, _i, _i64, _i64, _i64, _i64, _i64, _i]),
     "swvr_bwd_mixed": (_i, [_i, _i, _i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _f,
                             _p, _p, _p, _p, _i64, _p, _i, _p, _i, _p, _i, _p, _p, _sz, _p]),

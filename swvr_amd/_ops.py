@@ -68,6 +68,8 @@ def _embed(E, cdt):
 
 
 def _lead_stride(x):
+    if x.shape[1] == 0:  # empty rows (K = 0 or D = 0): any stride, 0 satisfies the ABI
+        return 0
     return x.stride(0) if x.shape[0] > 1 else x.shape[1]
 
 
@@ -144,6 +146,33 @@ def _forward(h, W, E, bias, logit_scale, chunk, cdt):
         rc = lib.swvr_fwd_mixed(tag, h_tag, w_tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc),
                                 _lead_stride(Wc), _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
                                 _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_of(h.device))
+    _lib.check(rc)
+    return O, lse
+
+
+def _forward_active(h, W, E, bias, weight, logit_scale, chunk, cdt):
+    """Readout of the tokens with a non-zero weight (swvr_fwd_active): O rows and lse of the
+    other tokens are 0, which leaves a weighted loss unchanged (their terms are weight x finite)."""
+    _require_device(h)
+    lib = _lib.load()
+    if cdt not in _lib.DTYPE_TAG:
+        raise NotImplementedError(f"swvr_amd: compute dtype {cdt} has no active-token forward")
+    N, K = h.shape
+    V, D = E.shape
+    Kp = _kpad(K)
+    (hc, h_tag), (Wc, w_tag), Ec = _operand(h, cdt, Kp), _operand(W, cdt, Kp), _embed(E, cdt)
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    w = weight.reshape(-1).to(torch.float32).contiguous()
+    O = torch.empty(N, D, dtype=torch.float32, device=h.device)
+    lse = torch.empty(N, dtype=torch.float32, device=h.device)
+    tag = _lib.DTYPE_TAG[cdt]
+    ws_bytes = lib.swvr_fwd_active_workspace_size(tag, N, Kp, V, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
+    with torch.cuda.device(h.device):
+        rc = lib.swvr_fwd_active(tag, h_tag, w_tag, N, Kp, V, D, _lib.ptr(hc), _lead_stride(hc), _lib.ptr(Wc),
+                                 _lead_stride(Wc), _lib.ptr(Ec), _lead_stride(Ec), _lib.ptr(b), float(logit_scale),
+                                 _lib.ptr(w), _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws_bytes,
+                                 _lib.stream_of(h.device))
     _lib.check(rc)
     return O, lse
 
@@ -251,12 +280,46 @@ def _autograd_backward(ctx, gO, glse):
 _fwd_op.register_autograd(_autograd_backward, setup_context=_setup_context)
 
 
+@torch.library.custom_op("swvr::chunked_fwd_active", mutates_args=())
+def _fwd_active_op(h: torch.Tensor, W: torch.Tensor, E: torch.Tensor, bias: Optional[torch.Tensor],
+                   weight: torch.Tensor, logit_scale: float, chunk: int,
+                   cdt: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _forward_active(h, W, E, bias, weight, logit_scale, chunk, cdt)
+
+
+@_fwd_active_op.register_fake
+def _(h, W, E, bias, weight, logit_scale, chunk, cdt):
+    return h.new_empty(h.shape[0], E.shape[1], dtype=torch.float32), h.new_empty(h.shape[0], dtype=torch.float32)
+
+
+def _setup_context_active(ctx, inputs, output):
+    h, W, E, bias, weight, logit_scale, chunk, cdt = inputs
+    _setup_context(ctx, (h, W, E, bias, logit_scale, chunk, cdt, True), output)
+
+
+def _autograd_backward_active(ctx, gO, glse):
+    gh, gW, gE, gb, *_ = _autograd_backward(ctx, gO, glse)
+    return gh, gW, gE, gb, None, None, None, None
+
+
+_fwd_active_op.register_autograd(_autograd_backward_active, setup_context=_setup_context_active)
+
+
 def softmax_readout_op(h2, W, E, bias, logit_scale, chunk, cdt):
     """``h2`` is ``[N, K]``; returns ``(O [N, D], LSE [N])`` in fp32 (swvr/chunked.py:208-212)."""
     if h2.device.type not in ("cuda", "cpu"):  # meta / fake tracing: no autocast state
         return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt, True)
     with torch.autocast(h2.device.type, enabled=False):
         return _fwd_op(h2, W, E, bias, float(logit_scale), int(chunk), cdt, True)
+
+
+def softmax_readout_active_op(h2, W, E, bias, weight, logit_scale, chunk, cdt):
+    """``softmax_readout_op`` for a weighted loss: tokens with ``weight == 0`` get O rows and lse
+    of 0 instead of their readout (``swvr_fwd_active``); ``weight`` is [N], no gradient."""
+    if h2.device.type not in ("cuda", "cpu"):
+        return _fwd_active_op(h2, W, E, bias, weight, float(logit_scale), int(chunk), cdt)
+    with torch.autocast(h2.device.type, enabled=False):
+        return _fwd_active_op(h2, W, E, bias, weight, float(logit_scale), int(chunk), cdt)
 
 
 # ---------------------------------------------------------------- fused MSE loss

@@ -10,7 +10,7 @@ import os
 import torch
 from torch import nn
 
-from ._ops import DEFAULT_CHUNK, REDUCTIONS, mse_loss_op, softmax_readout_op
+from ._ops import DEFAULT_CHUNK, REDUCTIONS, mse_loss_op, softmax_readout_active_op, softmax_readout_op
 
 
 def default_chunk_size():
@@ -73,8 +73,35 @@ def softmax_readout_mse(h, W, E, target, bias=None, *, weight=None, reduction="m
     weighted sum over the sum of the weights, or over the token count without weights),
     "sum", or "none" (the per-token values).
     """
-    O, lse = softmax_readout(h, W, E, bias, logit_scale=logit_scale, chunk_size=chunk_size)
+    if _skips_zero_weight(h, W, weight, reduction):
+        # The loss is weight x (a finite term) per token, so zero-weight tokens need no readout:
+        # the library computes the others only and gives these O rows and lse of 0, for which
+        # the term is finite again (swvr_fwd_active lists the rows it still computes to keep
+        # the reference's NaNs).
+        _check(h, W, E, bias)
+        lead = h.shape[:-1]
+        chunk = int(chunk_size) if chunk_size else default_chunk_size()
+        if chunk <= 0:
+            raise ValueError(f"chunk_size must be positive, got {chunk}")
+        O, lse = softmax_readout_active_op(h.reshape(-1, h.shape[-1]), W, E, bias, weight.reshape(-1),
+                                           logit_scale, chunk, _compute_dtype(h, W))
+        O, lse = O.view(*lead, E.shape[1]), lse.view(lead)
+    else:
+        O, lse = softmax_readout(h, W, E, bias, logit_scale=logit_scale, chunk_size=chunk_size)
     return _mse_loss(O, lse, target, weight, reduction, z_loss_weight)
+
+
+def _skips_zero_weight(h, W, weight, reduction):
+    """Whether the loss's readout may leave out zero-weight tokens: a per-token weight of exactly
+    the token shape on h's GPU, with no gradient of its own (its gradient would be each token's
+    loss), a known reduction, and a compute dtype the library's forward runs in."""
+    if not isinstance(weight, torch.Tensor) or not isinstance(h, torch.Tensor) or reduction not in REDUCTIONS:
+        return False
+    if h.device.type != "cuda" or weight.device != h.device or weight.shape != h.shape[:-1]:
+        return False
+    if weight.requires_grad or weight.is_complex() or h.shape[-1] != W.shape[-1] or W.dim() != 2:
+        return False
+    return _compute_dtype(h, W) in (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _mse_loss(O, lse, target, weight, reduction, z_loss_weight):

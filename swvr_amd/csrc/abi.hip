@@ -131,15 +131,17 @@ int check_storage(int dtype, int h_dtype, int w_dtype) {
 int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
                int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
                float logit_scale, float* O, float* lse, float* m_out, float* l_out, void* workspace,
-               size_t workspace_bytes, void* stream) {
+               size_t workspace_bytes, void* stream, const float* weight = nullptr) {
   g_err[0] = 0;
   int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
   if (rc != SWVR_OK) return rc;
   if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
   if (N > 0 && ((D > 0 && !O) || (m_out ? !l_out : !lse)))
     return fail(SWVR_EINVAL, m_out ? "m, l and acc must be non-null" : "O and lse must be non-null");
+  const bool active = weight != nullptr;
   FwdPlan plan;
-  if (!fwd_plan(dtype, N, K, V, D, &plan)) return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
+  if (!fwd_plan(dtype, N, K, V, D, &plan, active))
+    return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
   if (N == 0) return SWVR_OK;
   if (!workspace || workspace_bytes < plan.ws_bytes)
     return fail(SWVR_EWORKSPACE, "forward workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
@@ -158,8 +160,10 @@ int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_
   p.D = (int)D;
   p.h_f32 = h_dtype != dtype;
   p.w_f32 = w_dtype != dtype;
-  hipError_t e = fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, m_out, l_out,
-                            static_cast<hipStream_t>(stream));
+  hipError_t e = active ? fwd_launch_active(dtype, plan, p, weight, static_cast<char*>(workspace), O, lse,
+                                            static_cast<hipStream_t>(stream))
+                        : fwd_launch(dtype, plan, p, static_cast<char*>(workspace), O, lse, m_out, l_out,
+                                     static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "forward launch");
   return SWVR_OK;
 }
@@ -260,6 +264,25 @@ int swvr_fwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, in
                    float logit_scale, float* O, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   return fwd_common(dtype, h_dtype, w_dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr,
                     nullptr, workspace, workspace_bytes, stream);
+}
+
+size_t swvr_fwd_active_workspace_size(int dtype, int64_t N, int64_t K, int64_t V, int64_t D) {
+  FwdPlan plan;
+  if (N < 0 || V < 0 || D < 0 || !fwd_plan(dtype, N, K, V, D, &plan, true)) return 0;
+  return plan.ws_bytes;
+}
+
+int swvr_fwd_active(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
+                    int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
+                    float logit_scale, const float* weight, float* O, float* lse, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (N > 0 && !weight) {
+    g_err[0] = 0;
+    return fail(SWVR_EINVAL, "weight must be non-null");
+  }
+  static const float kNoTokens = 0.f;  // N = 0: any non-null pointer selects the active plan
+  return fwd_common(dtype, h_dtype, w_dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr,
+                    nullptr, workspace, workspace_bytes, stream, weight ? weight : &kNoTokens);
 }
 
 int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh,

@@ -1592,6 +1592,11 @@ size_t dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 
 }  // namespace
 
+hipError_t compact_tokens(const int* flag, int N, int* idx, int* inv, int* n_act, hipStream_t stream) {
+  bwd_compact_kernel<<<1, 1024, 0, stream>>>(flag, N, idx, inv, n_act);
+  return hipGetLastError();
+}
+
 bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chunk, bool need_gh, BwdPlan* plan,
               bool w_f32, int64_t K8) {
   const bool f8 = K8 > 0;

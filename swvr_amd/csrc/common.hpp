@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace swvr {
 
 typedef __bf16 bf16_t;
@@ -891,6 +893,24 @@ __device__ __forceinline__ uint4 load_chunk(const Src* p) {
   }
 }
 
+// Whether any of the CE values of T in a 16-byte chunk is an infinity or a NaN
+// (all exponent bits set).
+template <class T>
+__device__ __forceinline__ bool chunk_nonfinite(uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (sizeof(T) == 4) {
+      bad |= (w[i] & 0x7f800000u) == 0x7f800000u;
+    } else {
+      constexpr uint32_t m = std::is_same<T, f16_t>::value ? 0x7c00u : 0x7f80u;
+      bad |= (w[i] & m) == m || ((w[i] >> 16) & m) == m;
+    }
+  }
+  return bad;
+}
+
 // Token rows (h) packed in the LDS image of their operand tiles:
 // [N_pad / 32][S = K_pad / BK][32 rows][BK], each 16-byte chunk already at its
 // XOR-swizzled place (KTile layout), zeros past N and K.  A tile of any
@@ -899,10 +919,17 @@ __device__ __forceinline__ uint4 load_chunk(const Src* p) {
 // One workgroup per 32 rows x 8 slices: the rows are read as contiguous
 // 512-byte runs into LDS, the 8 slices written as one contiguous 16 KB run.
 // The source may be fp32 for a 2-byte T (rounded here); with rowmajor set,
-// the rows are also written as a plain [N][K] copy in T.
+// the rows are also written as a plain [N][K] copy in T.  With rows set, packed
+// row q is source row rows[q] for q < n_rows[0] and zero past it (a gather of
+// selected tokens in position order).  With nonfinite set, a workgroup that
+// packs an infinity or a NaN stores 1 there (every such store writes the same
+// value, so the word ends as 1 whatever their order).
 template <class Src, class T>
 __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restrict__ src, int64_t ld, int N, int K,
-                                                              int S, T* __restrict__ dst, T* __restrict__ rowmajor) {
+                                                              int S, T* __restrict__ dst, T* __restrict__ rowmajor,
+                                                              const int* __restrict__ rows,
+                                                              const int* __restrict__ n_rows,
+                                                              int* __restrict__ nonfinite) {
   constexpr int BK = SliceK<T>::value, CE = 16 / (int)sizeof(T), CPR = BK / CE;
   static_assert(CPR == 4, "4 chunks per slice row");
   constexpr int SPW = 8;                    // slices per workgroup
@@ -912,18 +939,23 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restr
   const int grp = blockIdx.x / SG, s0 = (blockIdx.x % SG) * SPW;
   const int ns = S - s0 < SPW ? S - s0 : SPW;
   const int t = threadIdx.x;
+  const int nr = rows ? n_rows[0] : N;
+  bool bad = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = i * 8 + t / 32, kc = t % 32;
-    const int64_t n = (int64_t)grp * 32 + row;
+    const int64_t q = (int64_t)grp * 32 + row;
+    const int64_t n = q < nr ? (rows ? (int64_t)rows[q] : q) : -1;
     const int k = (s0 * CPR + kc) * CE;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (kc < ns * CPR && n < N && k < K) {
+    if (kc < ns * CPR && n >= 0 && k < K) {
       v = load_chunk<Src, T>(src + n * ld + k);
       if (rowmajor) *reinterpret_cast<uint4*>(rowmajor + n * K + k) = v;
+      bad |= chunk_nonfinite<T>(v);
     }
     tile[row * RSTRIDE + kc] = v;
   }
+  if (nonfinite && __syncthreads_or(bad) && t == 0) nonfinite[0] = 1;
   __syncthreads();
   T* out = dst + ((int64_t)grp * S + s0) * 32 * BK;
 #pragma unroll
@@ -936,25 +968,33 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restr
 }
 
 // Pack rows [rows_pad][K] of src (rows_pad a multiple of 32) into the tile image.
+// Optional gather and non-finite flag: see pack_rows_tiled_kernel.
+struct PackExtra {
+  const int* rows = nullptr;
+  const int* n_rows = nullptr;
+  int* nonfinite = nullptr;
+};
+
 template <class T, class Src = T>
 __host__ hipError_t launch_pack_rows(const Src* src, int64_t ld, int N, int K, int S, int64_t rows_pad, T* dst,
-                                     hipStream_t stream, T* rowmajor = nullptr) {
+                                     hipStream_t stream, T* rowmajor = nullptr, PackExtra x = PackExtra()) {
   const int64_t blocks = (rows_pad / 32) * ((S + 7) / 8);
   if (blocks == 0) return hipSuccess;
-  pack_rows_tiled_kernel<Src, T><<<(unsigned)blocks, 256, 0, stream>>>(src, ld, N, K, S, dst, rowmajor);
+  pack_rows_tiled_kernel<Src, T><<<(unsigned)blocks, 256, 0, stream>>>(src, ld, N, K, S, dst, rowmajor, x.rows,
+                                                                       x.n_rows, x.nonfinite);
   return hipGetLastError();
 }
 
 // launch_pack_rows from a source in T, or in fp32 for a 2-byte T.
 template <class T>
 __host__ hipError_t pack_src(const void* src, int f32, int64_t ld, int rows, int K, int S, int64_t rows_pad, T* dst,
-                    hipStream_t stream, T* rowmajor = nullptr) {
+                    hipStream_t stream, T* rowmajor = nullptr, PackExtra x = PackExtra()) {
   if constexpr (sizeof(T) == 2) {
     if (f32)
       return launch_pack_rows<T, float>(static_cast<const float*>(src), ld, rows, K, S, rows_pad, dst, stream,
-                                        rowmajor);
+                                        rowmajor, x);
   }
-  return launch_pack_rows<T>(static_cast<const T*>(src), ld, rows, K, S, rows_pad, dst, stream, rowmajor);
+  return launch_pack_rows<T>(static_cast<const T*>(src), ld, rows, K, S, rows_pad, dst, stream, rowmajor, x);
 }
 
 // Loads of a KTile of R token rows (from n0, multiple of 32) from packed rows.

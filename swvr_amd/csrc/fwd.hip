@@ -15,6 +15,7 @@
 //     feeds acc^T += E^T P^T straight from the score registers;
 //   * partials (m, l, acc) of all waves and splits are merged by
 //     fwd_combine_kernel in a fixed order (deterministic).
+#include <cmath>
 #include <type_traits>
 
 #include "common.hpp"
@@ -123,11 +124,18 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
 
   const int lane = lane_id(), w = (int)(threadIdx.x >> 6);
   const int wv = w / C::WT, wt = w % C::WT;
+  int n_tb = p.n_tb, n_split = p.n_split, ntok = p.N;  // ntok: token rows of a partial
+  if (p.n_act) {
+    n_tb = p.n_act[3];
+    n_split = p.n_act[4];
+    if ((int)blockIdx.x >= n_tb * n_split) return;
+    ntok = n_tb * BM;
+  }
   int split, tb;
-  grouped_tile(blockIdx.x, p.n_split, p.n_tb, &split, &tb);
+  grouped_tile(blockIdx.x, n_split, n_tb, &split, &tb);
   const int n0 = tb * BM;
-  const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
-  const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
+  const int vt_begin = (int)((int64_t)split * p.n_vt / n_split);
+  const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / n_split);
   const T* Ep = static_cast<const T*>(p.Ep);
 
   float m[FT], l[FT];
@@ -292,17 +300,17 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
     const int n = n0 + wt * WTR + ft * 32 + (ln & 31);
-    if (n < p.N) {
+    if (n < ntok) {
       if (ln < 32) {
-        p.part_m[(int64_t)part * p.N + n] = m[ft];
-        p.part_l[(int64_t)part * p.N + n] = l[ft];
+        p.part_m[(int64_t)part * ntok + n] = m[ft];
+        p.part_l[(int64_t)part * ntok + n] = l[ft];
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int d = db * 32 + c_row(r, ln);
-          p.part_acc[((int64_t)part * DP + d) * p.N + n] = oacc[db][ft][r];
+          p.part_acc[((int64_t)part * DP + d) * ntok + n] = oacc[db][ft][r];
         }
     }
   }
@@ -339,11 +347,18 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
 
   const int lane = lane_id(), w = wave_id();
   const int wv = w / C::WT, wt = w % C::WT;
+  int n_tb = p.n_tb, n_split = p.n_split, ntok = p.N;  // ntok: token rows of a partial
+  if (p.n_act) {
+    n_tb = p.n_act[3];
+    n_split = p.n_act[4];
+    if ((int)blockIdx.x >= n_tb * n_split) return;
+    ntok = n_tb * BM;
+  }
   int split, tb;
-  grouped_tile(blockIdx.x, p.n_split, p.n_tb, &split, &tb);
+  grouped_tile(blockIdx.x, n_split, n_tb, &split, &tb);
   const int n0 = tb * BM;
-  const int vt_begin = (int)((int64_t)split * p.n_vt / p.n_split);
-  const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / p.n_split);
+  const int vt_begin = (int)((int64_t)split * p.n_vt / n_split);
+  const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / n_split);
   const T* Ep = static_cast<const T*>(p.Ep);
 
   float m[FT], l[FT];
@@ -493,17 +508,17 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
     const int n = n0 + wt * WTR + ft * 32 + (ln & 31);
-    if (n < p.N) {
+    if (n < ntok) {
       if (ln < 32) {
-        p.part_m[(int64_t)part * p.N + n] = m[ft];
-        p.part_l[(int64_t)part * p.N + n] = l[ft];
+        p.part_m[(int64_t)part * ntok + n] = m[ft];
+        p.part_l[(int64_t)part * ntok + n] = l[ft];
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int d = db * 32 + c_row(r, ln);
-          p.part_acc[((int64_t)part * DP + d) * p.N + n] = oacc[db][ft][r];
+          p.part_acc[((int64_t)part * DP + d) * ntok + n] = oacc[db][ft][r];
         }
     }
   }
@@ -518,6 +533,25 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
 // merged partial (M, L and the unnormalised acc, [N][D]) instead of O / LSE.
 // One thread per (d, n) with n fastest; the d = 0 thread of a row also writes
 // its LSE (or M, L).
+// Merge of one (row, column) over n_part partials: m / l of partial q at
+// pm[q * sml] / pl[q * sml], its acc at pa[q * sp] (read when has_d).
+__device__ __forceinline__ void merge_partials(const float* __restrict__ pm, const float* __restrict__ pl,
+                                               const float* __restrict__ pa, int n_part, int64_t sml, int64_t sp,
+                                               bool has_d, float* M_, float* L_, float* a_) {
+  float M = kNegInf;
+  for (int q = 0; q < n_part; ++q) M = fmaxf(M, pm[q * sml]);
+  const float shift = M == kNegInf ? 0.f : M;
+  float L = 0.f, a = 0.f;
+  for (int q = 0; q < n_part; ++q) {
+    const float wq = expf(pm[q * sml] - shift);
+    L += pl[q * sml] * wq;
+    if (has_d) a += pa[q * sp] * wq;
+  }
+  *M_ = M;
+  *L_ = L;
+  *a_ = a;
+}
+
 __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restrict__ part_m,
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_acc, int n_part, int N,
@@ -528,15 +562,8 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   const int Dw = D > 0 ? D : 1;
   if (e >= (int64_t)N * Dw) return;
   const int d = (int)(e / N), n = (int)(e % N);
-  float M = kNegInf;
-  for (int q = 0; q < n_part; ++q) M = fmaxf(M, part_m[(int64_t)q * N + n]);
-  const float shift = M == kNegInf ? 0.f : M;
-  float L = 0.f, a = 0.f;
-  for (int q = 0; q < n_part; ++q) {
-    const float wq = expf(part_m[(int64_t)q * N + n] - shift);
-    L += part_l[(int64_t)q * N + n] * wq;
-    if (d < D) a += part_acc[q * sp + d * sd + n * sn] * wq;
-  }
+  float M, L, a;
+  merge_partials(part_m + n, part_l + n, part_acc + d * sd + n * sn, n_part, N, sp, d < D, &M, &L, &a);
   if (m_out) {
     if (d < D) O[(int64_t)n * ldo + d] = a;
     if (d == 0) {
@@ -549,11 +576,109 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   }
 }
 
+// fwd_combine_kernel of the active-token forward: token n merges the partials
+// of its position inv[n] (WV x n_split partials of n_tb x BM rows each, n_tb and
+// n_split at n_act[3], n_act[4]); a token outside the active set gets an O row
+// of 0 and LSE 0.
+__global__ __launch_bounds__(256) void fwd_combine_active_kernel(
+    const float* __restrict__ part_m, const float* __restrict__ part_l, const float* __restrict__ part_acc,
+    const int* __restrict__ inv, const int* __restrict__ n_act, int BM, int WV, int N, int D, int DP,
+    float* __restrict__ O, int64_t ldo, float* __restrict__ lse) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int Dw = D > 0 ? D : 1;
+  if (e >= (int64_t)N * Dw) return;
+  const int d = (int)(e / N), n = (int)(e % N);
+  const int q = inv[n];
+  if (q < 0) {
+    if (d < D) O[(int64_t)n * ldo + d] = 0.f;
+    if (d == 0) lse[n] = 0.f;
+    return;
+  }
+  const int tb = n_act[3], sp = n_act[4];
+  const int64_t rows = (int64_t)tb * BM;
+  float M, L, a;
+  merge_partials(part_m + q, part_l + q, part_acc + d * rows + q, WV * sp, rows, (int64_t)DP * rows, d < D, &M, &L,
+                 &a);
+  if (d < D) O[(int64_t)n * ldo + d] = a / L;
+  if (d == 0) lse[n] = M + logf(L);
+}
+
+// The active-token forward's token blocks and vocabulary splits (active_grid)
+// from the count, into n_act[3], n_act[4]: once per call, for every kernel.
+__global__ __launch_bounds__(64) void fwd_active_grid_kernel(int* __restrict__ n_act, int BM, int n_tb_max,
+                                                             int n_split0, int n_vt) {
+  if (threadIdx.x == 0) {
+    int tb, sp;
+    active_grid(n_act[0], BM, n_tb_max, n_split0, n_vt, &tb, &sp);
+    n_act[3] = tb;
+    n_act[4] = sp;
+  }
+}
+
+// Flags of the active-token forward's parameter checks, bad[0..1]:
+// bad[0] = 1 when the logit scale is not finite, E holds an infinity or a NaN
+// or the bias a NaN or +inf (W is checked as it is packed); bad[1] starts at 1
+// when there is a bias (or no vocabulary) and drops to 0 once a bias entry
+// above -inf is seen (every entry -inf makes every score -inf).
+__global__ __launch_bounds__(64) void fwd_flags_init_kernel(int* __restrict__ bad, int scale_bad, int bias_all_neg) {
+  if (threadIdx.x == 0) {
+    bad[0] = scale_bad;
+    bad[1] = bias_all_neg;
+  }
+}
+
+// Grid-stride scan of E's V x D elements and the bias for fwd_flags_init_kernel's
+// words.  Every store writes the same value, so the words end the same
+// whatever the order of the stores.
+template <class T>
+__global__ __launch_bounds__(256) void fwd_param_scan_kernel(const T* __restrict__ E, int64_t lde, int V, int D,
+                                                             const float* __restrict__ bias, int* __restrict__ bad) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  bool nf = false, live = false;
+  if (D > 0)
+    for (int64_t e = t0; e < (int64_t)V * D; e += stride) {
+      const int64_t v = e / D;
+      nf |= !__builtin_isfinite((float)E[v * lde + (e - v * D)]);
+    }
+  if (bias)
+    for (int64_t v = t0; v < V; v += stride) {
+      const float b = bias[v];
+      nf |= b != b || b == kPosInf;
+      live |= b > kNegInf;
+    }
+  if (__syncthreads_or(nf) && threadIdx.x == 0) bad[0] = 1;
+  if (__syncthreads_or(live) && threadIdx.x == 0) bad[1] = 0;
+}
+
+// flag[n] = 1 for a token of the active-token forward: a non-zero (or NaN)
+// weight, an h row holding an infinity or a NaN (in the compute dtype), or a
+// flagged parameter (bad[0] or bad[1]: then every token).  One wave per token;
+// only a zero-weight token's row is read, in 16-byte chunks.
+template <class Src, class T>
+__global__ __launch_bounds__(256) void fwd_active_flag_kernel(const float* __restrict__ weight,
+                                                              const Src* __restrict__ h, int64_t ldh, int N, int K,
+                                                              const int* __restrict__ bad, int* __restrict__ flag) {
+  const int n = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (n >= N) return;
+  const int lane = lane_id();
+  bool act = weight[n] != 0.f || bad[0] != 0 || bad[1] != 0;  // NaN != 0
+  if (!act) {  // uniform over the wave
+    constexpr int CE = 16 / (int)sizeof(T);
+    bool nf = false;
+    for (int c = lane; c < K / CE; c += 64)
+      nf |= chunk_nonfinite<T>(load_chunk<Src, T>(h + (int64_t)n * ldh + (int64_t)c * CE));
+    act = __ballot(nf) != 0;
+  }
+  if (lane == 0) flag[n] = act ? 1 : 0;
+}
+
 template <class T, int DP, bool F8 = false>
 hipError_t launch_tile(const FwdPlan& plan, const FwdParams& p, hipStream_t stream) {
   typedef FwdCfg<T, DP, F8> C;
   if (plan.BV != C::BV || plan.BM != C::BM) return hipErrorInvalidValue;
-  const int blocks = plan.n_tb * plan.n_split;
+  // the active-token forward may use up to twice the all-token grid (active_grid); the rest exit at once
+  const int blocks = plan.n_tb * plan.n_split * (p.n_act ? 2 : 1);
   timing_begin(kKindFwdTile, stream);
   if constexpr (!F8 && FwdTile<T, DP>::stream_e)
     fwd_stream_kernel<T, DP><<<blocks, C::NT, 0, stream>>>(p);
@@ -633,8 +758,10 @@ hipError_t pack(const FwdParams& p, const FwdPlan& plan, hipStream_t stream) {
 
 }  // namespace
 
-bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan) {
+bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan, bool active) {
   (void)K;
+  if (active && dtype == kFP8) return false;
+  plan->active = active;
   // Widest embedding slice of one pass: 256 (2-byte dtypes), 128 (fp32, e4m3).  A wider D runs
   // in slices of that width, each pass recomputing the same scores for its columns of E.
   const int DS = dtype == kBF16 || dtype == kF16 ? 256 : 128;
@@ -681,13 +808,17 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   }
   plan->n_split = n_split;
   plan->n_part = WV * n_split;
+  plan->WV = WV;
+  // token rows of a partial: N; the active-token forward's partials hold up to
+  // 2 x n_tb x n_split workgroups' n_tb x BM positions each (active_grid)
+  const int64_t NR = active ? 2 * (int64_t)plan->n_tb * BM : N;
   size_t off = 0;
   plan->off_m = off;
-  off += align256((size_t)plan->n_part * N * 4);
+  off += align256((size_t)plan->n_part * NR * 4);
   plan->off_l = off;
-  off += align256((size_t)plan->n_part * N * 4);
+  off += align256((size_t)plan->n_part * NR * 4);
   plan->off_acc = off;
-  off += align256((size_t)plan->n_part * N * 4 * DP);
+  off += align256((size_t)plan->n_part * NR * 4 * DP);
   plan->off_Ep = off;
   off += align256((size_t)plan->V_pad * DP * tbytes);
   plan->off_bias = off;
@@ -698,6 +829,17 @@ bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* pl
   off += align256((size_t)plan->N_pad * plan->hS * (tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value) * tbytes);
   plan->off_Wp = off;
   off += align256((size_t)plan->V_pad * plan->hS * (tbytes == 4 ? SliceK<float>::value : SliceK<bf16_t>::value) * tbytes);
+  plan->off_flag = plan->off_idx = plan->off_inv = plan->off_nact = 0;
+  if (active) {
+    plan->off_flag = off;
+    off += align256((size_t)N * 4);
+    plan->off_idx = off;
+    off += align256((size_t)N * 4);
+    plan->off_inv = off;
+    off += align256((size_t)N * 4);
+    plan->off_nact = off;  // [0] count, [1..2] parameter flags
+    off += 256;
+  }
   plan->ws_bytes = off;
   return true;
 }
@@ -745,6 +887,103 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
     fwd_combine_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
         p.part_m, p.part_l, p.part_acc, plan.n_part, p.N, q.D, (int64_t)plan.DP * p.N, p.N, 1, O ? O + d0 : nullptr,
         D, lse, m_out, l_out);
+    timing_end(kKindFwdCombine, stream);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+namespace {
+
+template <class T>
+hipError_t active_setup(const FwdPlan& plan, const FwdParams& p, const float* weight, int* flag, int* idx, int* inv,
+                        int* n_act, int* bad, hipStream_t stream) {
+  timing_begin(kKindPack, stream);
+  const bool scale_bad = !std::isfinite(p.scale);
+  fwd_flags_init_kernel<<<1, 64, 0, stream>>>(bad, scale_bad ? 1 : 0, (p.bias || p.V == 0) ? 1 : 0);
+  hipError_t e = hipGetLastError();
+  // W once (as fwd_launch packs it), checked for non-finite values on the way
+  PackExtra wx;
+  wx.nonfinite = bad;
+  T* const Wp = const_cast<T*>(static_cast<const T*>(p.Wp));
+  if (e == hipSuccess) e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream, nullptr, wx);
+  const int64_t work = (int64_t)p.V * (p.D > 0 ? p.D : 1);
+  if (e == hipSuccess && work > 0 && (p.D > 0 || p.bias)) {
+    const int blocks = (int)((work + 255) / 256 < 2048 ? (work + 255) / 256 : 2048);
+    fwd_param_scan_kernel<T><<<blocks, 256, 0, stream>>>(static_cast<const T*>(p.E), p.lde, p.V, p.D, p.bias, bad);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) {
+    const unsigned blocks = (unsigned)((p.N + 3) / 4);
+    if (sizeof(T) == 2 && p.h_f32)
+      fwd_active_flag_kernel<float, T><<<blocks, 256, 0, stream>>>(weight, static_cast<const float*>(p.h), p.ldh,
+                                                                   p.N, p.K, bad, flag);
+    else
+      fwd_active_flag_kernel<T, T><<<blocks, 256, 0, stream>>>(weight, static_cast<const T*>(p.h), p.ldh, p.N, p.K,
+                                                               bad, flag);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = compact_tokens(flag, p.N, idx, inv, n_act, stream);
+  if (e == hipSuccess) {
+    fwd_active_grid_kernel<<<1, 64, 0, stream>>>(n_act, plan.BM, plan.n_tb, plan.n_split, plan.n_vt);
+    e = hipGetLastError();
+  }
+  // h rows of the active tokens in position order, zeros past them
+  PackExtra hx;
+  hx.rows = idx;
+  hx.n_rows = n_act;
+  T* const hp = const_cast<T*>(static_cast<const T*>(p.hp));
+  if (e == hipSuccess) e = pack_src<T>(p.h, p.h_f32, p.ldh, p.N, p.K, plan.hS, plan.N_pad, hp, stream, nullptr, hx);
+  timing_end(kKindPack, stream);
+  return e;
+}
+
+}  // namespace
+
+hipError_t fwd_launch_active(int dtype, const FwdPlan& plan, FwdParams p, const float* weight, char* ws, float* O,
+                             float* lse, hipStream_t stream) {
+  if (p.N == 0) return hipSuccess;
+  if (!plan.active || dtype == kFP8) return hipErrorInvalidValue;
+  p.n_tb = plan.n_tb;
+  p.n_split = plan.n_split;
+  p.n_vt = plan.n_vt;
+  p.part_m = reinterpret_cast<float*>(ws + plan.off_m);
+  p.part_l = reinterpret_cast<float*>(ws + plan.off_l);
+  p.part_acc = reinterpret_cast<float*>(ws + plan.off_acc);
+  p.Ep = ws + plan.off_Ep;
+  p.biasp = reinterpret_cast<const float*>(ws + plan.off_bias);
+  p.hp = ws + plan.off_hp;
+  p.Wp = ws + plan.off_Wp;
+  p.hS = plan.hS;
+  int* flag = reinterpret_cast<int*>(ws + plan.off_flag);
+  int* idx = reinterpret_cast<int*>(ws + plan.off_idx);
+  int* inv = reinterpret_cast<int*>(ws + plan.off_inv);
+  int* n_act = reinterpret_cast<int*>(ws + plan.off_nact);
+  p.n_act = n_act;
+  hipError_t e;
+  switch (dtype) {
+    case kBF16: e = active_setup<bf16_t>(plan, p, weight, flag, idx, inv, n_act, n_act + 1, stream); break;
+    case kF16: e = active_setup<f16_t>(plan, p, weight, flag, idx, inv, n_act, n_act + 1, stream); break;
+    case kF32: e = active_setup<float>(plan, p, weight, flag, idx, inv, n_act, n_act + 1, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess) return e;
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  const int D = p.D;
+  for (int d0 = 0; d0 < (D > 0 ? D : 1); d0 += plan.DS) {
+    FwdParams q = p;
+    q.E = static_cast<const char*>(p.E) + d0 * esz;
+    q.D = D - d0 < plan.DS ? D - d0 : plan.DS;
+    switch (dtype) {
+      case kBF16: e = pack_et<bf16_t>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<bf16_t>(plan, q, stream); break;
+      case kF16: e = pack_et<f16_t>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<f16_t>(plan, q, stream); break;
+      default: e = pack_et<float>(q, plan, stream); if (e == hipSuccess) e = dispatch_dp<float>(plan, q, stream); break;
+    }
+    if (e != hipSuccess) return e;
+    timing_begin(kKindFwdCombine, stream);
+    const int64_t n_threads = (int64_t)p.N * (q.D > 0 ? q.D : 1);
+    fwd_combine_active_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
+        p.part_m, p.part_l, p.part_acc, inv, n_act, plan.BM, plan.WV, p.N, q.D, plan.DP, O + d0, D, lse);
     timing_end(kKindFwdCombine, stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

@@ -51,7 +51,44 @@ struct FwdParams {
   int h_f32, w_f32;    // h / W stored in fp32 (rounded to the compute dtype as they are packed)
   const float* h_scale;  // e4m3 forward: [1] dequantisation scale of h, else null
   const float* w_scale;  // e4m3 forward: [V] dequantisation scales of W's rows, else null
+  // Active-token forward: [0] the count of active tokens, whose rows are packed
+  // in position order (hp), [3] / [4] the token blocks and vocabulary splits
+  // (active_grid), all on the device; null: every token, at its own row.
+  const int* n_act;
 };
+
+// Token blocks and vocabulary splits of an active-token forward, from the
+// device count of active tokens.  The launch has grid = n_tb_max x n_split0
+// workgroups (the all-token tiling: whole rounds of kFwdRound, one workgroup
+// per CU); with n_act active tokens the first n_tb x n_split of them work.  The
+// split count minimises the forward's duration in the round model, rounds x
+// vocabulary tiles per workgroup ~ ceil(n_tb x s / kFwdRound) / s, over
+// s = n_split0 .. min(n_vt / 2, 2 x grid / n_tb) (the smallest such s on a
+// tie): the partial buffers hold 2 x grid workgroups' partials.  Computed once
+// per call (fwd_active_grid_kernel) into the count's block, so every kernel of
+// the forward uses the same values and the host needs no copy of them.
+constexpr int kFwdRound = 256;
+__host__ __device__ inline void active_grid(int n_act, int BM, int n_tb_max, int n_split0, int n_vt, int* n_tb,
+                                            int* n_split) {
+  int tb = n_act <= 0 ? 0 : (n_act + BM - 1) / BM;
+  if (tb > n_tb_max) tb = n_tb_max;
+  int sp = n_split0;
+  if (tb > 0) {
+    const int cap = n_vt / 2 > 1 ? n_vt / 2 : 1;
+    const int64_t fit = 2 * (int64_t)n_tb_max * n_split0 / tb;
+    const int hi = fit < cap ? (int)fit : cap;
+    int64_t best_r = ((int64_t)tb * sp + kFwdRound - 1) / kFwdRound;
+    for (int s = n_split0 + 1; s <= hi; ++s) {
+      const int64_t r = ((int64_t)tb * s + kFwdRound - 1) / kFwdRound;
+      if (r * sp < best_r * s) {  // r / s < best_r / sp
+        best_r = r;
+        sp = s;
+      }
+    }
+  }
+  *n_tb = tb;
+  *n_split = sp;
+}
 
 struct FwdPlan {
   int BV, BM, DP;
@@ -61,6 +98,11 @@ struct FwdPlan {
   int64_t N_pad;         // token rows of the packed h
   int hS;                // reduction slices of the packed h and W
   size_t off_m, off_l, off_acc, off_Ep, off_bias, off_hp, off_Wp, ws_bytes;
+  // active-token forward: per-token flags, positions, the count and the
+  // non-finite parameter flag (ws_bytes includes them only when planned so)
+  bool active;
+  int WV;
+  size_t off_flag, off_idx, off_inv, off_nact;
 };
 
 // fwd_plan / fwd_launch dtype of the e4m3 forward (h, W in e4m3; E in bf16).
@@ -68,11 +110,21 @@ constexpr int kFwdFP8 = 3;
 
 // Tile shape, split count and workspace for a forward call; ok=false if the
 // dtype / D combination is unsupported.
-bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan);
+bool fwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, FwdPlan* plan, bool active = false);
 // O / lse, or with m_out / l_out set the merged partial softmax (m, l, and the
 // unnormalised acc in O) of the vocabulary rows given.
 hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, float* O, float* lse, float* m_out,
                       float* l_out, hipStream_t stream);
+// The forward of the tokens with a non-zero weight (weight: fp32 [N]); O rows
+// and lse of the others are 0.  A zero-weight token whose h row holds an
+// infinity or a NaN stays active, and so does every token when W, E or the
+// bias holds a NaN or +inf or when every bias entry is -inf: the rows whose
+// loss the reference makes NaN (0 * NaN) are computed.  Plan with active set.
+hipError_t fwd_launch_active(int dtype, const FwdPlan& plan, FwdParams p, const float* weight, char* ws, float* O,
+                             float* lse, hipStream_t stream);
+// Order-preserving compaction of flagged tokens (flag[n] != 0): idx[q] = token
+// of position q, inv[n] = position of token n or -1, n_act[0] = count.
+hipError_t compact_tokens(const int* flag, int N, int* idx, int* inv, int* n_act, hipStream_t stream);
 // Merge S vocabulary shards' partials (m, l: [S][N]; acc: [S][N][D]) in shard order.
 hipError_t shard_combine(int S, int N, int D, const float* m, const float* l, const float* acc, float* O, float* lse,
                          hipStream_t stream);
