@@ -10,10 +10,11 @@ A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
 Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd TFLOP/s,
 2 N V (4K + 3D) / step time — the FLOPs of the reference's algorithm with one
-score recompute (docs/DESIGN.md:39); ``ms_per_step`` is the step time.  The
-backward skips tokens whose cotangents are all zero (weight 0 in the loss):
-``bwd_active_tokens`` says how many it ran over, ``work_tflops`` counts only
-the FLOPs done, and the per-kernel rates and the roofline are priced on them.
+score recompute (docs/DESIGN.md:39); ``ms_per_step`` is the step time.  Both
+passes skip tokens of weight 0 in the loss (their loss terms are 0 x finite, so
+the forward leaves their readout out and their cotangents are zero):
+``active_tokens`` says how many they ran over, ``work_tflops`` counts only the
+FLOPs done, and the per-kernel rates and the roofline are priced on them.
 
 The dominant kernel's roofline is measured live: every launch in the timed
 region is bracketed by HIP events on its own stream (the C ABI's timing
@@ -87,13 +88,14 @@ def algorithmic_flops(N, K, V, D):
 def kernel_flops(name, N, K, V, D, n_act=None, de_in_gemm=False):
     """Algorithmic FLOPs of all launches of one kernel kind over one step.
 
-    The backward runs over the ``n_act`` tokens whose cotangents are not all
-    zero (zero-weight tokens contribute nothing), so its kernels are priced on
-    the work they do: n_act tokens.  ``de_in_gemm``: the wide-embedding scores
-    kernel stages P and the gradient GEMM launch forms dE = P^T gO."""
+    Both passes run over the ``n_act`` tokens of non-zero weight (a zero-weight
+    token's loss term is 0 x finite: no readout, zero cotangents), so the kernels
+    are priced on the work they do: n_act tokens.  ``de_in_gemm``: the
+    wide-embedding scores kernel stages P and the gradient GEMM launch forms
+    dE = P^T gO."""
     nb = N if n_act is None else n_act
     if name == "fwd_tile_kernel":
-        return 2.0 * N * V * (K + D)             # S = h W^T, P E
+        return 2.0 * nb * V * (K + D)            # S = h W^T, P E
     if name == "bwd_scores_kernel":
         # S recompute, dP = gO E^T (and dE = P^T gO unless the GEMM launch forms it)
         return 2.0 * nb * V * (K + (1 if de_in_gemm else 2) * D)
@@ -142,12 +144,12 @@ def measured_traffic(t, config, kernel):
 
 def algorithmic_bytes(name, N, K, V, D, chunk, n_act, wide):
     """Bytes one launch must move at least: each operand read once, each result written once.
-    fwd: h, W, E in, O and lse out.  scores (a chunk of C rows): h of the active tokens, W_c, E_c,
+    fwd: h of the active tokens, W, E in, O and lse (every token) out.  scores (a chunk of C rows): h of the active tokens, W_c, E_c,
     gO in; the dS stage (and the P stage of the wide kernel) out.  gradient GEMM (a chunk): the dS
     stage, h, W_c in; gW_c out; the fp32 dh accumulator read and written."""
     C = min(chunk, V)
     if name == "fwd_tile_kernel":
-        return 2 * (N * K + V * K + V * D) + 4 * N * (D + 1)
+        return 2 * (n_act * K + V * K + V * D) + 4 * N * (D + 1)
     if name == "bwd_scores_kernel":
         return 2 * (n_act * K + C * K + C * D + n_act * D) + 2 * C * n_act * (2 if wide else 1)
     if name == "bwd_gemm_kernel":
@@ -419,7 +421,7 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     fp8 = (fp8_path(h, W, E, b, target, weight, cfg["z"], args.chunk, params, fwd_flops, flops, fwd_iters)
            if D <= 128 and not args.no_fp8 else None)
-    # tokens with a non-zero weight: the others have zero cotangents, and the
+    # tokens with a non-zero weight: the forward leaves the others out and the
     # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
     n_act = int((weight != 0).sum().item()) if weight is not None else N
     de_in_gemm = _lib.bwd_tiling(torch.bfloat16, N, K, V, D, args.chunk)["kernel"] == 2
@@ -458,8 +460,8 @@ def main():
                                + (", bias" if cfg["bias"] else "") + (f", weight {cfg['weight']}" if cfg["weight"] else "")
                                + (f", z_loss {cfg['z']}" if cfg["z"] else ""),
                    "N": N, "K": K, "V": V, "D": D, "chunk": args.chunk},
-        "bwd_active_tokens": n_act,
-        "work_tflops": round((fwd_flops + (flops - fwd_flops) * n_act / N) / (ms * 1e-3) / 1e12, 1),
+        "active_tokens": n_act,
+        "work_tflops": round(flops * n_act / N / (ms * 1e-3) / 1e12, 1),
         "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
         "peak_gib": round(peak_gib, 3),

@@ -837,11 +837,11 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
 }
 
 // Workgroup index -> (row, col) of an R x Q tile grid such that the 32
-// workgroups an XCD runs together cover a 4 x 8 patch (4 rows, 8 columns):
-// blocks go to the XCDs round-robin, xcd_swizzle gives each XCD a contiguous
-// range of the tile order, and the order walks 4-row column strips.
+// workgroups an XCD runs together cover a G x (32 / G) patch (G rows): blocks
+// go to the XCDs round-robin, xcd_swizzle gives each XCD a contiguous range of
+// the tile order, and the order walks G-row column strips.
+template <int G = 4>
 __device__ __forceinline__ void grouped_tile(int b, int R, int Q, int* row, int* col) {
-  constexpr int G = 4;
   const int t = xcd_swizzle(b, R * Q);
   const int group = t / (G * Q), first = group * G;
   const int gsize = min(R - first, G);
