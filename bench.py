@@ -172,11 +172,14 @@ def traffic_summary(root):
             for r in csv.DictReader(open(f)):
                 if r["Counter_Name"] != counter:
                     continue
-                m = re.search(r"(fwd_tile_kernel|bwd_scores_ring_kernel|bwd_scores_wide_kernel|bwd_scores_kernel|"
-                              r"bwd_gemm_kernel|elementwise_kernel|copy)", r["Kernel_Name"])
+                m = re.search(r"(fwd_tile_kernel|fwd_stream_kernel|bwd_scores_ring_kernel|bwd_scores_wide_kernel|"
+                              r"bwd_scores_kernel|bwd_gemm_kernel|elementwise_kernel|copy)", r["Kernel_Name"])
                 if not m:
                     continue
-                k = "bwd_scores_kernel" if m.group(1).startswith("bwd_scores") else m.group(1)
+                # the launch-timing kinds: both forward kernels are "fwd_tile_kernel", every scores
+                # kernel "bwd_scores_kernel"
+                k = ("bwd_scores_kernel" if m.group(1).startswith("bwd_scores") else
+                     "fwd_tile_kernel" if m.group(1).startswith("fwd_") else m.group(1))
                 acc.setdefault(k, []).append(float(r["Counter_Value"]))
         return {k: sum(v) / len(v) for k, v in acc.items()}, {k: len(v) for k, v in acc.items()}
 
