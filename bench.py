@@ -5,6 +5,7 @@
     python bench.py --no-cpu             # skip the CPU baseline leg
     python bench.py --copy-probe-mib 1024  # only a plain device copy (HBM counter calibration)
     python bench.py --mfma-probe         # only the matrix-core probe (the power / clock ceiling)
+    python bench.py --library-gemm       # only hipBLASLt (torch.mm) on the gradient GEMMs' shapes
 
 A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
@@ -283,6 +284,36 @@ def mfma_probe(iters=1 << 20, launches=3):
     return res
 
 
+def library_gemm(cfg, chunk, reps=10):
+    """Calibration of the gradient GEMMs against the vendor library: torch.mm (hipBLASLt on ROCm)
+    on one chunk's two products at this configuration's shape, dW_c = dS_c^T h (C x Q)(Q x K) and
+    dh = dS_c W_c (Q x C)(C x K) with fp32 and bf16 outputs, Q = the bench's active tokens rounded
+    to 32 as the library's GEMM runs them, N(0,1) bf16 operands.  Measurement only: the product's
+    gradient GEMMs are this repository's own kernel (bwd_gemm_kernel), which forms both in one launch."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    _, _, _, _, _, weight, _ = make_inputs(cfg, "cuda")
+    n_act = int((weight != 0).sum().item()) if weight is not None else cfg["N"]
+    Q, C, K = (n_act + 31) // 32 * 32, min(chunk, cfg["V"]), cfg["K"]
+    r = lambda *s: torch.randn(*s, device="cuda", generator=g).to(torch.bfloat16)
+    S, h, Wc = r(C, Q), r(Q, K), r(C, K)
+    St = S.t().contiguous()
+    flops = 2.0 * C * Q * K
+    res = {"shape": {"C": C, "Q": Q, "K": K}}
+    for name, fn in (("dW_bf16_out", lambda: torch.mm(S, h)), ("dh_bf16_out", lambda: torch.mm(St, Wc)),
+                     ("dh_fp32_out", lambda: torch.mm(St, Wc, out_dtype=torch.float32))):
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / reps
+        res[name] = {"ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    return res
+
+
 def fp8_path(h, W, E, b, target, weight, z, chunk, params, fwd_flops, flops, iters):
     """The opt-in e4m3 path (swvr_amd.fp8) on the same inputs, reported beside the bf16 line
     (not part of it).  Forward: W quantised once, as a server would keep it; each call quantises
@@ -351,12 +382,17 @@ def main():
     ap.add_argument("--traffic-from", default=None,
                     help="print the traffic summary (profiles/readout_traffic.json) built from rocprofv3 "
                          "counter runs under this directory, and exit")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only time torch.mm (hipBLASLt) on the config's gradient GEMM shapes (calibration)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run only the matrix-core probe (swvr_probe_mfma: the bare MFMA step with random, zero "
                          "and LDS-fed operands) and print its rates")
     args = ap.parse_args()
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.library_gemm:
+        print(json.dumps({"library_gemm": library_gemm(CONFIGS[args.config], args.chunk)}), flush=True)
         return
     if args.mfma_probe:
         print(json.dumps({"mfma_probe_summary": mfma_probe()}), flush=True)
