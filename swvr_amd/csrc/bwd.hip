@@ -1295,26 +1295,57 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
 }
 
 // ---------------------------------------------------------------- dE / db
-// One thread per (row, d) of gE plus one per row of gb; consecutive threads
-// take consecutive rows, so the partial reads are coalesced.
-// G_de: partials of dE ([G_de][DP][C]; 1 when the gradient GEMM formed dE^T
-// whole), G: partials of db ([G][C]).
+// gE and gb rows of a chunk from their partials, summed over the partials in a
+// fixed order (g ascending).  G_de: partials of dE ([G_de][DP][C]; 1 when the
+// gradient GEMM formed dE^T whole), G: partials of db ([G][C]).  One workgroup
+// per tile of kRedV chunk rows x kRedD columns: the partial reads run along the
+// rows (consecutive v, as the partials store them), the sums pass through LDS,
+// and gE is written along its rows (consecutive d), so both sides coalesce.  The
+// workgroups of column tile 0 also write gb of their rows.
+constexpr int kRedV = 32, kRedD = 16;
+
+// sum_{g < n} p[g * stride] in order g = 0, 1, ...; the loads go out in batches of 8
+// ahead of their adds, so a long sum waits for memory once per batch, not once per term.
+__device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int g0 = 0; g0 < n; g0 += 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = g0 + u < n ? p[(int64_t)(g0 + u) * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (g0 + u < n) s += x[u];
+  }
+  return s;
+}
+
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict__ part_dE,
                                                          const float* __restrict__ part_db, int G_de, int G, int C,
                                                          int DP, int v0, int cv, int D, void* gE, int gE_dtype,
                                                          float* gb) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n_e = gE ? (int64_t)cv * D : 0;
-  if (e < n_e) {
-    const int d = (int)(e / cv), v = (int)(e % cv);
-    float s = 0.f;
-    for (int g = 0; g < G_de; ++g) s += part_dE[((int64_t)g * DP + d) * C + v];
-    store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, s);
-  } else if (gb && e < n_e + cv) {
-    const int v = (int)(e - n_e);
-    float s = 0.f;
-    for (int g = 0; g < G; ++g) s += part_db[(int64_t)g * C + v];
-    gb[v0 + v] = s;
+  __shared__ float tile[kRedV][kRedD + 1];  // padded: the transposed accesses stay conflict-free
+  const int vb = blockIdx.x * kRedV, db0 = blockIdx.y * kRedD;
+  const int t = threadIdx.x;
+  if (gE) {
+#pragma unroll
+    for (int j = 0; j < kRedV * kRedD / 256; ++j) {
+      const int i = j * 256 + t;
+      const int dl = i / kRedV, vl = i % kRedV;  // consecutive threads: consecutive rows
+      const int v = vb + vl, d = db0 + dl;
+      tile[vl][dl] = v < cv && d < D ? ordered_sum(part_dE + (int64_t)d * C + v, (int64_t)DP * C, G_de) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRedV * kRedD / 256; ++j) {
+      const int i = j * 256 + t;
+      const int vl = i / kRedD, dl = i % kRedD;  // consecutive threads: consecutive columns
+      const int v = vb + vl, d = db0 + dl;
+      if (v < cv && d < D) store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, tile[vl][dl]);
+    }
+  }
+  if (gb && blockIdx.y == 0 && t < kRedV) {
+    const int v = vb + t;
+    if (v < cv) gb[v0 + v] = ordered_sum(part_db + v, C, G);
   }
 }
 
@@ -1555,8 +1586,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     }
     if (p.gE || p.gb) {
       timing_begin(kKindBwdReduce, stream);
-      const int64_t n_threads = (p.gE ? (int64_t)cv * p.D : 0) + (p.gb ? cv : 0);
-      bwd_reduce_kernel<<<(int)((n_threads + 255) / 256), 256, 0, stream>>>(
+      const dim3 grid((unsigned)((cv + kRedV - 1) / kRedV),
+                      p.gE && p.D > 0 ? (unsigned)((p.D + kRedD - 1) / kRedD) : 1u);
+      bwd_reduce_kernel<<<grid, 256, 0, stream>>>(
           part_dE, part_db, plan.kind == kScoresWide ? 1 : plan.n_gpart, plan.n_gpart, (int)plan.C, plan.DP, v0, cv,
           p.D, p.gE, p.gE_dtype, p.gb);
       timing_end(kKindBwdReduce, stream);

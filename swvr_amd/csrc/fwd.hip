@@ -534,18 +534,39 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
 // One thread per (d, n) with n fastest; the d = 0 thread of a row also writes
 // its LSE (or M, L).
 // Merge of one (row, column) over n_part partials: m / l of partial q at
-// pm[q * sml] / pl[q * sml], its acc at pa[q * sp] (read when has_d).
+// pm[q * sml] / pl[q * sml], its acc at pa[q * sp] (read when has_d).  The
+// loads go out in batches of 8 ahead of the arithmetic, which runs in partial
+// order, so the merge waits for memory once per batch, not once per partial.
 __device__ __forceinline__ void merge_partials(const float* __restrict__ pm, const float* __restrict__ pl,
                                                const float* __restrict__ pa, int n_part, int64_t sml, int64_t sp,
                                                bool has_d, float* M_, float* L_, float* a_) {
+  constexpr int B = 8;
   float M = kNegInf;
-  for (int q = 0; q < n_part; ++q) M = fmaxf(M, pm[q * sml]);
+  for (int q0 = 0; q0 < n_part; q0 += B) {
+    float x[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) x[u] = q0 + u < n_part ? pm[(q0 + u) * sml] : kNegInf;
+#pragma unroll
+    for (int u = 0; u < B; ++u) M = fmaxf(M, x[u]);
+  }
   const float shift = M == kNegInf ? 0.f : M;
   float L = 0.f, a = 0.f;
-  for (int q = 0; q < n_part; ++q) {
-    const float wq = expf(pm[q * sml] - shift);
-    L += pl[q * sml] * wq;
-    if (has_d) a += pa[q * sp] * wq;
+  for (int q0 = 0; q0 < n_part; q0 += B) {
+    float xm[B], xl[B], xa[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const bool in = q0 + u < n_part;
+      xm[u] = in ? pm[(q0 + u) * sml] : 0.f;
+      xl[u] = in ? pl[(q0 + u) * sml] : 0.f;
+      xa[u] = in && has_d ? pa[(q0 + u) * sp] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (q0 + u < n_part) {
+        const float wq = expf(xm[u] - shift);
+        L += xl[u] * wq;
+        if (has_d) a += xa[u] * wq;
+      }
   }
   *M_ = M;
   *L_ = L;
