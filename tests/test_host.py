@@ -311,3 +311,34 @@ def test_bwd_tiling_reports_the_scores_kernel_plan():
     assert b"chunk" in lib.swvr_last_error()
     assert lib.swvr_bwd_tiling(9, 16, 16, 16, 16, 64, out, 7) == _lib.EDTYPE
     assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 64, None, 7) == _lib.EINVAL
+
+
+def test_abi_active_forward_checks_arguments_without_touching_the_device():
+    """swvr_fwd_active (the weighted loss's forward over its non-zero-weight tokens)."""
+    lib = _lib.load()
+    N, K, V, D = 3000, 256, 5000, 64
+    full = lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, D)
+    act = lib.swvr_fwd_active_workspace_size(_lib.BF16, N, K, V, D)
+    # twice the partial rows (the count's re-split) plus flags, positions and the count block
+    assert act > full and act - full < full
+    assert lib.swvr_fwd_active_workspace_size(3, N, K, V, D) == 0          # no e4m3 active forward
+    assert lib.swvr_fwd_active_workspace_size(_lib.F32, N, K, V, 300) > 0  # fp32, D in slices
+    p = ctypes.c_void_p(16)
+
+    def call(n=N, weight=p, ws=act, wsp=p, dtype=_lib.BF16):
+        return lib.swvr_fwd_active(dtype, dtype, dtype, n, K, V, D, p, K, p, K, p, D, None, 1.0, weight,
+                                   p, p, wsp, ws, None)
+
+    assert call(weight=None) == _lib.EINVAL and b"weight" in lib.swvr_last_error()
+    assert call(ws=act - 256) == _lib.EWORKSPACE
+    assert call(dtype=9) == _lib.EDTYPE
+    assert call(n=0, weight=None, ws=0, wsp=None) == _lib.OK  # no tokens: nothing to do
+
+
+def test_the_loss_skips_zero_weight_readouts_only_on_the_gpu_path():
+    from swvr_amd.api import _skips_zero_weight
+    h, W = torch.randn(8, 16), torch.randn(40, 16)
+    w = torch.ones(8)
+    assert not _skips_zero_weight(h, W, w, "mean")  # CPU tensors: the op raises, as every other path
+    hm, Wm, wm = h.to("meta"), W.to("meta"), w.to("meta")
+    assert not _skips_zero_weight(hm, Wm, wm, "mean")
