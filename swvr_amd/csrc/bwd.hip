@@ -1520,6 +1520,16 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   for (int c = 0; c < plan.n_chunks; ++c) {
     const int v0 = (int)(c * plan.C);
     const int cv = (int)((p.V - v0) < plan.C ? (p.V - v0) : plan.C);
+    // A partial last chunk has fewer vocabulary tiles: more token groups fill the chip with it
+    // (G from the same rule as the plan's).  Its partials use its own width as their row stride,
+    // so G_c x width stays within the buffers' G x C.
+    const int n_vtc = (cv + plan.BV - 1) / plan.BV;
+    const int Cc = n_vtc * plan.BV;
+    int Gc = plan.wgs == 256 ? plan.wgs / n_vtc : (plan.wgs + n_vtc - 1) / n_vtc;
+    if (Gc > plan.n_tb) Gc = plan.n_tb;
+    if ((int64_t)Gc * Cc > (int64_t)plan.G * plan.C) Gc = (int)((int64_t)plan.G * plan.C / Cc);
+    if (Gc < plan.G) Gc = plan.G;  // a full chunk: the plan's G
+    const int n_gpart_c = plan.n_gpart / plan.G * Gc;
     ScoresParams sp;
     sp.hp = hp;
     sp.Wp = Wp;
@@ -1536,10 +1546,10 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.N_pad = (int)plan.N_pad;
     sp.v0 = v0;
     sp.cv = cv;
-    sp.C = (int)plan.C;
+    sp.C = Cc;
     sp.n_tb = plan.n_tb;
-    sp.G = plan.G;
-    sp.n_vtc = (cv + plan.BV - 1) / plan.BV;
+    sp.G = Gc;
+    sp.n_vtc = n_vtc;
     sp.stage = stage;
     sp.pstage = pstage;
     sp.n_tb32 = (int)(plan.N_pad / 32);
@@ -1575,7 +1585,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.gOp = gOp;
       gp.DP = plan.DP;
       gp.part_dE = part_dE;
-      gp.C = (int)plan.C;
+      gp.C = Cc;
       gp.gW = p.gW;
       gp.gW_dtype = p.gW_dtype;
       gp.dh_acc = dh_acc;
@@ -1589,7 +1599,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       const dim3 grid((unsigned)((cv + kRedV - 1) / kRedV),
                       p.gE && p.D > 0 ? (unsigned)((p.D + kRedD - 1) / kRedD) : 1u);
       bwd_reduce_kernel<<<grid, 256, 0, stream>>>(
-          part_dE, part_db, plan.kind == kScoresWide ? 1 : plan.n_gpart, plan.n_gpart, (int)plan.C, plan.DP, v0, cv,
+          part_dE, part_db, plan.kind == kScoresWide ? 1 : n_gpart_c, n_gpart_c, Cc, plan.DP, v0, cv,
           p.D, p.gE, p.gE_dtype, p.gb);
       timing_end(kKindBwdReduce, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1693,6 +1703,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   if (G > plan->n_tb) G = plan->n_tb;
   if (G < 1) G = 1;
   plan->G = G;
+  plan->wgs = wgs;
   plan->n_gpart = G * WT;  // db (and, but for the wide kernel, dE) partials: one per token group and token-wave row
   plan->kind = kind;
   plan->dh_acc = need_gh;

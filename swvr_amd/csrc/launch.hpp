@@ -138,7 +138,8 @@ struct BwdPlan {
   int64_t N_pad;         // token stride of the dS stage
   int64_t C;             // vocabulary rows per chunk (multiple of BV)
   int n_chunks;
-  int G;                 // token groups of the dS kernel
+  int G;                 // token groups of the dS kernel (a full chunk)
+  int wgs;               // workgroups the dS kernel's tiling fills the chip with (G per chunk from it)
   int n_gpart;           // dE / db partials per chunk
   int kind;              // scores kernel: kScoresGeneral, kScoresRing (narrow), kScoresWide
   bool dh_acc;           // dh accumulates in fp32 (over the active tokens), then expands into gh
