@@ -148,6 +148,27 @@ def test_torch_compile_matches_eager_and_stays_chunked():
     assert extra < N * V * 2
 
 
+def test_torch_compile_of_the_weighted_loss_matches_eager():
+    """A token weight routes the loss through swvr::chunked_fwd_active (the forward over the
+    non-zero-weight tokens): its fake and autograd registrations trace in one graph."""
+    N, K, V, D, C = 2048, 256, 16384, 32, 4096
+    h, W, E, b = make(N, K, V, D, torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    target = torch.randn(N, D, device="cuda", generator=g)
+    weight = (torch.rand(N, device="cuda", generator=g) >= 0.25).float()
+    fn = lambda h: swvr.softmax_readout_mse(h, W, E, target, b, weight=weight, z_loss_weight=1e-3, chunk_size=C)
+    torch._dynamo.reset()
+    cfn = torch.compile(fn, fullgraph=True)
+    loss_c = cfn(h)
+    g_c = torch.autograd.grad(loss_c, (h, W, E, b))
+    loss_e = fn(h)
+    g_e = torch.autograd.grad(loss_e, (h, W, E, b))
+    assert rel_err(loss_c, loss_e) < 1e-5
+    for a, r in zip(g_c, g_e):
+        assert rel_err(a, r) < 1e-3
+    assert torch.count_nonzero(g_c[0][weight == 0]) == 0  # zero-weight tokens: no gradient
+
+
 def test_gradients_are_deterministic():
     inputs = make(700, 512, 20000, 64, torch.bfloat16)
     gO, glse = torch.randn(700, 64, device="cuda"), torch.randn(700, device="cuda")
