@@ -131,14 +131,13 @@ int check_storage(int dtype, int h_dtype, int w_dtype) {
 int fwd_common(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h,
                int64_t ldh, const void* W, int64_t ldw, const void* E, int64_t lde, const float* bias,
                float logit_scale, float* O, float* lse, float* m_out, float* l_out, void* workspace,
-               size_t workspace_bytes, void* stream, const float* weight = nullptr) {
+               size_t workspace_bytes, void* stream, bool active = false, const float* weight = nullptr) {
   g_err[0] = 0;
   int rc = check_common(dtype, N, K, V, D, h, ldh, W, ldw, E, lde);
   if (rc != SWVR_OK) return rc;
   if ((rc = check_storage(dtype, h_dtype, w_dtype)) != SWVR_OK) return rc;
   if (N > 0 && ((D > 0 && !O) || (m_out ? !l_out : !lse)))
     return fail(SWVR_EINVAL, m_out ? "m, l and acc must be non-null" : "O and lse must be non-null");
-  const bool active = weight != nullptr;
   FwdPlan plan;
   if (!fwd_plan(dtype, N, K, V, D, &plan, active))
     return fail(SWVR_EDTYPE, "no forward kernel for dtype %d, D=%lld", dtype, (long long)D);
@@ -280,9 +279,8 @@ int swvr_fwd_active(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, i
     g_err[0] = 0;
     return fail(SWVR_EINVAL, "weight must be non-null");
   }
-  static const float kNoTokens = 0.f;  // N = 0: any non-null pointer selects the active plan
   return fwd_common(dtype, h_dtype, w_dtype, N, K, V, D, h, ldh, W, ldw, E, lde, bias, logit_scale, O, lse, nullptr,
-                    nullptr, workspace, workspace_bytes, stream, weight ? weight : &kNoTokens);
+                    nullptr, workspace, workspace_bytes, stream, true, weight);
 }
 
 int swvr_fwd_partial(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, const void* h, int64_t ldh,
