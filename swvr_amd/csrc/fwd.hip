@@ -916,6 +916,11 @@ hipError_t fwd_launch(int dtype, const FwdPlan& plan, FwdParams p, char* ws, flo
 
 namespace {
 
+// Everything of the active-token forward before its passes: the parameter flags (bad[0..1], set
+// while W is packed and by the E / bias scan), the per-token flags and their compaction into
+// positions (idx, inv, n_act[0]), the device-side token blocks and splits (n_act[3..4]), and the
+// active tokens' h rows packed in position order.  n_act points at the count block:
+// [0] count, [1..2] parameter flags, [3..4] token blocks and splits.
 template <class T>
 hipError_t active_setup(const FwdPlan& plan, const FwdParams& p, const float* weight, int* flag, int* idx, int* inv,
                         int* n_act, int* bad, hipStream_t stream) {
