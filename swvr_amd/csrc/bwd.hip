@@ -646,29 +646,42 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 
     TG tgl;  // layout only
     TE tel;
+    // dP block (fv, ft) = gO[tokens] E[rows]^T over D.  Every lane-dependent
+    // offset in the epilogue derives from an opaque copy of the lane's row (see
+    // opaque_zero), so it is recomputed per block: hoisted out of the block loop
+    // the offsets would be spilled, and each reload from scratch waits (vmcnt in
+    // order) for every store issued before it.  The side tiles sit in the three
+    // slots before and at the current one.
+    auto dp_block = [&](int fv, int ft) {
+      const int ln = lane + opaque_zero();
+      const int lr = ln & 31;
+      const char* sGe = smem + ((slot_gt + NS - 1) % NS) * SB;
+      const char* sEe = smem + ((slot_gt + NS - 2) % NS) * SB;
+      f32x16_t d = zero16();
+#pragma unroll
+      for (int kd = 0; kd < DK; ++kd)
+        mfma_k16(d, read_op(tgl, sGe, wt * WTR + ft * 32 + lr, kd, ln),
+                 read_op(tel, sEe, wv * WVR + fv * 32 + lr, kd, ln));
+      return d;
+    };
+    // software-pipelined by one block: the dP products of the next block run
+    // on the matrix cores while this block's exponentials and stores run
+    f32x16_t dp_next = dp_block(0, 0);
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv) {
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
-        // Every lane-dependent offset below derives from an opaque copy of the
-        // lane's row (see opaque_zero), so it is recomputed here, per block:
-        // hoisted out of the block loop they would be spilled, and each reload
-        // from scratch waits (vmcnt in order) for every store issued before it.
+        f32x16_t dp = dp_next;
+        constexpr int kBlocks = FV * FT;
+        const int nb = fv * FT + ft + 1;
+        if (nb < kBlocks) dp_next = dp_block(nb / FT, nb % FT);
         const int ln = lane + opaque_zero();
         const int lr = ln & 31;
         const int vl = wv * WVR + fv * 32 + lr;  // tile-local row of this lane
-        // the side tiles sit in the three slots before and at the current one
         const char* sGte = smem + slot_gt * SB;
-        const char* sGe = smem + ((slot_gt + NS - 1) % NS) * SB;
-        const char* sEe = smem + ((slot_gt + NS - 2) % NS) * SB;
         const float* sLe = sLD + (blk & 1) * (2 * BM);
         const float* sDe = sLe + BM;
         const int tr0 = wt * WTR + ft * 32;  // first token of the block
-        // dP block = gO[tokens] E[rows]^T over D
-        f32x16_t dp = zero16();
-#pragma unroll
-        for (int kd = 0; kd < DK; ++kd)
-          mfma_k16(dp, read_op(tgl, sGe, tr0 + lr, kd, ln), read_op(tel, sEe, vl, kd, ln));
         float dbs = 0.f;
         const float2 bm = F8 ? sBM[vl] : make_float2(bvv[fv], p.scale);  // this lane's row: bias, score factor
 #pragma unroll
