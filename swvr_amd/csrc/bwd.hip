@@ -752,24 +752,26 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
 
 // ---------------------------------------------------------------- scores, wide embeddings
 // bf16 / f16 with DP > 64 and fp32 with DP > 128 (DP any multiple of the
-// slice width: 32 elements, 16 for fp32): 128 tokens x 256 vocabulary rows per workgroup of
-// 8 waves (2 token halves x 4 vocabulary quarters, 64 x 64 each).  Per token
-// block the ring carries the nk K-slices of h and W (-> S), then the DP / 32
-// D-slices of gO and E (-> dP = gO E^T), all as uniform 24 KB stages, so no
-// side tile is pinned in LDS and the next block's slices keep streaming
-// through the epilogue.  The epilogue stages dS and P in the compute dtype (P
+// slice width: 32 elements, 16 for fp32): 256 tokens (fp32: 128) x 256 vocabulary rows per
+// workgroup of 8 waves (2 token halves x 4 vocabulary quarters: 128 x 64 each, 0.75 operand reads
+// per MFMA; fp32 64 x 64).  Per token block the ring carries the nk K-slices of h and W (-> S),
+// then the DP / 32 D-slices of gO and E (-> dP = gO E^T) once per 64 tokens of a wave's rows (a
+// wave holds S for all its rows but dP for 64 of them: both whole would take 256 registers), all
+// as uniform 32 KB stages (fp32: 24 KB), so no side tile is pinned in LDS and the next block's
+// slices keep streaming through the epilogue.  The epilogue stages dS and P in the compute dtype (P
 // rounded as the reference rounds it for dE, swvr/triton_kernels.py:113);
 // dE^T = gO^T P is a product of the gradient GEMM launch over all active
 // positions, so no dE accumulator lives in registers; db is a per-wave
 // register partial.  LSE / delta sit in a double-buffered LDS strip, the bias
 // in registers.
+template <class T>
 struct ScoresWideTile {
-  static constexpr int BM = 128, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
+  static constexpr int BM = sizeof(T) == 2 ? 256 : 128, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
 };
 
 template <class T>
 __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
-  typedef ScoresWideTile C;
+  typedef ScoresWideTile<T> C;
   constexpr int kBK = SliceK<T>::value;
   constexpr int BM = C::BM, BV = C::BV, NT = C::NT, NS = C::NS;
   constexpr int WTR = BM / C::WT, WVR = BV / C::WV;  // rows per wave
@@ -783,8 +785,9 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   constexpr int SB = TA::BYTES + TB::BYTES;
   constexpr int L = TA::NI + TB::NI;  // loads per thread per stage
   constexpr int FT = WTR / 32, FV = WVR / 32;
+  constexpr int NPASS = FT / 2;  // dP passes per token block, 64 of a wave's rows each
   const int DP = p.DP;        // a multiple of the slice width kBK
-  const int ND = DP / kBK;    // D-slices per token block
+  const int ND = DP / kBK;    // D-slices per dP pass
 
   __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4];
   const float* const sLD = reinterpret_cast<const float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
@@ -811,7 +814,7 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   }
 
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
-  const int per_blk = nk + ND;
+  const int per_blk = nk + NPASS * ND;
   const int total = n_blocks * per_blk;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsL = lds0 + NS * SB;
@@ -826,6 +829,7 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP);
   // issue cursor over the walk: stage `issued` is (block is_blk, sub-stage
   // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk.. the D-slices
+  // of each dP pass in turn
   int issued = 0, is_blk = 0, is_sub = 0, is_slot = 0;
   auto issue_next = [&]() {
     if (issued >= total) return;
@@ -845,7 +849,7 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
       tw.issue(st + TA::BYTES, is_sub * kBK);
     } else {
       if (is_sub == nk) tg.base = reinterpret_cast<const char*>(gOp + (int64_t)n0 * DP);
-      const int d0 = (is_sub - nk) * kBK;
+      const int d0 = ((is_sub - nk) % ND) * kBK;
       tg.issue(st, d0);
       te.issue(st + TA::BYTES, d0);
     }
@@ -859,7 +863,7 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue_next();
 
-  f32x16_t sacc[FT][FV], dacc[FT][FV];
+  f32x16_t sacc[FT][FV], dacc[2][FV];
   Ring<NS> ring{NS - 1, total};  // the first publish_next() moves to stage 0, slot 0
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int n0 = (tb_begin + blk) * BM;
@@ -871,44 +875,48 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
 #pragma unroll
       for (int fv = 0; fv < FV; ++fv) sacc[ft][fv] = zero16();
     tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
-    ring.template publish_next<L>();  // D-slice 0
-#pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-      for (int fv = 0; fv < FV; ++fv) dacc[ft][fv] = zero16();
-    tile_reduce<T, kBK, L>(dacc, tg, te, smem, SB, ring, ND, wt * WTR, wv * WVR, issue_next);
 
     const float* sLe = sLD + (blk & 1) * (2 * BM);
     const float* sDe = sLe + BM;
 #pragma unroll
-    for (int fv = 0; fv < FV; ++fv) {
+    for (int ps = 0; ps < NPASS; ++ps) {
+      ring.template publish_next<L>();  // D-slice 0 of this pass
 #pragma unroll
-      for (int ft = 0; ft < FT; ++ft) {
-        const int ln = lane + opaque_zero();  // offsets recomputed per block (see opaque_zero)
-        const int vl = wv * WVR + fv * 32 + (ln & 31);  // tile-local row of this lane
-        const int tr0 = wt * WTR + ft * 32;             // first token of the block
-        float dbs = 0.f;
+      for (int f2 = 0; f2 < 2; ++f2)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
-          const int tl = tr0 + 8 * g4 + (ln >> 5) * 4;
-          const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
-          const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+        for (int fv = 0; fv < FV; ++fv) dacc[f2][fv] = zero16();
+      tile_reduce<T, kBK, L>(dacc, tg, te, smem, SB, ring, ND, wt * WTR + ps * 64, wv * WVR, issue_next);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * g4 + i;
-            const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv[fv]) - lv[i]);
-            const float ds = pv * (dacc[ft][fv][r] - dv[i]);
-            dbs += ds;
-            sacc[ft][fv][r] = pv;
-            dacc[ft][fv][r] = ds;  // the gradient GEMMs apply the scale (swvr/chunked.py:143-144)
+      for (int fv = 0; fv < FV; ++fv) {
+#pragma unroll
+        for (int f2 = 0; f2 < 2; ++f2) {
+          const int ft = 2 * ps + f2;
+          const int ln = lane + opaque_zero();  // offsets recomputed per block (see opaque_zero)
+          const int vl = wv * WVR + fv * 32 + (ln & 31);  // tile-local row of this lane
+          const int tr0 = wt * WTR + ft * 32;             // first token of the block
+          float dbs = 0.f;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            // registers 4g..4g+3 hold tokens 8g + 4(lane/32) + 0..3 of the block
+            const int tl = tr0 + 8 * g4 + (ln >> 5) * 4;
+            const float4 l4 = *reinterpret_cast<const float4*>(sLe + tl);
+            const float4 d4 = *reinterpret_cast<const float4*>(sDe + tl);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = 4 * g4 + i;
+              const float pv = fast_exp(fmaf(sacc[ft][fv][r], p.scale, bvv[fv]) - lv[i]);
+              const float ds = pv * (dacc[f2][fv][r] - dv[i]);
+              dbs += ds;
+              sacc[ft][fv][r] = pv;
+              dacc[f2][fv][r] = ds;  // the gradient GEMMs apply the scale (swvr/chunked.py:143-144)
+            }
           }
+          dbacc[fv] += dbs;
+          if (p.need_stage) store_ds_block<T>(dacc[f2][fv], p.stage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
+          if (p.need_dE) store_ds_block<T>(sacc[ft][fv], p.pstage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
+          sched_fence();
         }
-        dbacc[fv] += dbs;
-        if (p.need_stage) store_ds_block<T>(dacc[ft][fv], p.stage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
-        if (p.need_dE) store_ds_block<T>(sacc[ft][fv], p.pstage, p.n_tb32, vl0 + vl, n0 + tr0, ln);
-        sched_fence();
       }
     }
   }
@@ -1408,7 +1416,7 @@ hipError_t launch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_
 template <class T>
 hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStream_t stream) {
   if (plan.kind == kScoresWide) {
-    typedef ScoresWideTile C;
+    typedef ScoresWideTile<T> C;
     if (sp.multp || plan.BM != C::BM || plan.BV != C::BV || plan.DP % SliceK<T>::value != 0)
       return hipErrorInvalidValue;
     timing_begin(kKindBwdScores, stream);
@@ -1681,10 +1689,10 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
     WT = ScoresRingTile<bf16_t, 64>::WT;
     wgs = 256;
   } else if (kind == kScoresWide) {
-    BM = ScoresWideTile::BM;
-    BV = ScoresWideTile::BV;
-    WT = ScoresWideTile::WT;
-    wgs = 256;  // one workgroup per CU (its ring takes 96 KB of LDS)
+    BM = two ? ScoresWideTile<bf16_t>::BM : ScoresWideTile<float>::BM;
+    BV = ScoresWideTile<bf16_t>::BV;
+    WT = ScoresWideTile<bf16_t>::WT;
+    wgs = 256;  // one workgroup per CU (its ring takes 132 KB of LDS, fp32 100 KB)
   } else if (two) {
     general_tile<bf16_t, 128>(&BM, &BV, &WT, &wgs);
   } else if (DP == 32) {

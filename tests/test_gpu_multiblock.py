@@ -101,20 +101,21 @@ def run_case(h, W, E, b, gO, glse, chunk):
 
 
 # (dtype, N, K, V, D, chunk): narrow ring kernel (2-byte dtypes, D <= 64), wide kernel
-# (2-byte dtypes above 64, fp32 above 128, including widths beyond one forward pass: the
-# forward runs slices of E's columns) and general kernel (fp32 up to 128), token counts that leave a partial last block, vocabularies
-# with a partial last chunk, and a small chunk (G = 32) whose groups get 2 or 3 blocks.
+# (2-byte dtypes above 64 in 256-token blocks, fp32 above 128 in 128-token blocks, including
+# widths beyond one forward pass: the forward runs slices of E's columns) and general kernel
+# (fp32 up to 128), token counts that leave a partial last block, vocabularies with a partial
+# last chunk, and a small chunk (G = 32) whose groups get 2 or 3 blocks.
 CASES = [
     ("ring-bf16-D64", bf16, 8192 + 77, 256, 8192 + 300, 64, 8192),
     ("ring-bf16-D16", bf16, 8192 + 256, 128, 8192, 16, 8192),
     ("ring-f16-D48", f16, 9000, 192, 4096 + 64, 48, 4096),
     ("ring-bf16-chunk2048", bf16, 16384 + 5, 128, 4096 + 17, 64, 2048),
     ("wide-bf16-D128", bf16, 4096 + 33, 256, 8192 + 128, 128, 8192),
-    ("wide-f16-D200", f16, 2048 + 100, 128, 8192, 200, 8192),
-    ("wide-bf16-D256", bf16, 2048 + 64, 256, 8192 + 40, 256, 8192),
-    ("wide-bf16-D300", bf16, 2048 + 64, 256, 8192 + 100, 300, 8192),
-    ("wide-f16-D520", f16, 2048 + 5, 128, 8192, 520, 8192),
-    ("wide-bf16-D80", bf16, 2048 + 31, 192, 8192, 80, 8192),
+    ("wide-f16-D200", f16, 4096 + 100, 128, 8192, 200, 8192),
+    ("wide-bf16-D256", bf16, 4096 + 64, 256, 8192 + 40, 256, 8192),
+    ("wide-bf16-D300", bf16, 4096 + 64, 256, 8192 + 100, 300, 8192),
+    ("wide-f16-D520", f16, 4096 + 5, 128, 8192, 520, 8192),
+    ("wide-bf16-D80", bf16, 4096 + 31, 192, 8192, 80, 8192),
     ("wide-f32-D200", f32, 2048 + 1, 64, 8192, 200, 8192),
     ("general-f32-D64", f32, 2048 + 9, 128, 8192, 64, 8192),
     ("general-f32-D128", f32, 2048 + 3, 64, 4096, 128, 4096),

@@ -297,14 +297,14 @@ def test_bwd_tiling_reports_the_scores_kernel_plan():
     t = _lib.bwd_tiling(torch.bfloat16, 16384, 2560, 151936, 64, 8192)
     assert t == dict(BM=256, BV=256, G=8, C=8192, n_chunks=19, DP=64, kernel=1)
     t = _lib.bwd_tiling(torch.bfloat16, 32768, 4096, 256000, 256, 8192)
-    assert (t["BM"], t["BV"], t["G"], t["DP"], t["kernel"]) == (128, 256, 8, 256, 2)
+    assert (t["BM"], t["BV"], t["G"], t["DP"], t["kernel"]) == (256, 256, 8, 256, 2)
     t = _lib.bwd_tiling(torch.float32, 2051, 64, 4096, 128, 4096)
     assert (t["BM"], t["G"], t["C"], t["kernel"]) == (64, 16, 4096, 0)
     # beyond the old caps: the wide kernel streams any multiple of 32 (fp32: 16) columns
     assert (_lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 300, 512)["DP"], _lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 300, 512)["kernel"]) == (320, 2)
     assert _lib.bwd_tiling(torch.bfloat16, 64, 64, 512, 100, 512)["DP"] == 128
     t = _lib.bwd_tiling(torch.float32, 64, 64, 512, 200, 512)
-    assert (t["DP"], t["kernel"]) == (208, 2)
+    assert (t["BM"], t["DP"], t["kernel"]) == (128, 208, 2)   # fp32: 128-token blocks
     lib = _lib.load()
     out = (ctypes.c_int64 * 7)()
     assert lib.swvr_bwd_tiling(_lib.BF16, 16, 16, 16, 16, 0, out, 7) == _lib.EINVAL
