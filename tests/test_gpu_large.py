@@ -1,4 +1,4 @@
-"""Sizes past 32-bit element offsets: h with more than 2^31 elements.
+"""Sizes past 32-bit element offsets: h, and W, with more than 2^31 elements.
 
 N = 2^20 + 37 tokens of K = 2048 put h (and the backward's h over positions,
 its packed copy, the fp32 dh accumulator and gh) past 2^31 elements, so every
@@ -28,8 +28,13 @@ def rel_err(a, r):
 
 
 def cosine(a, r):
-    a, r = a.detach().double().flatten(), r.detach().double().flatten()
-    return (a @ r / (a.norm() * r.norm()).clamp_min(1e-300)).item()
+    """Cosine similarity, accumulated over pieces (a BLAS dot takes at most 2^31 - 1 elements)."""
+    a, r = a.detach().flatten(), r.detach().flatten()
+    dot = aa = rr = 0.0
+    for i in range(0, a.numel(), 1 << 28):
+        x, y = a[i:i + (1 << 28)].double(), r[i:i + (1 << 28)].double()
+        dot, aa, rr = dot + (x @ y).item(), aa + (x @ x).item(), rr + (y @ y).item()
+    return dot / max((aa * rr) ** 0.5, 1e-300)
 
 
 def inputs(seed):
@@ -114,3 +119,29 @@ def test_weighted_loss_at_more_than_2_31_hidden_elements():
         assert errs[n] <= 2e-2, errs
     for a, r in ((gW, rW), (gE, rE), (gb, rb)):
         assert cosine(a, r) >= 0.999
+
+
+def test_more_than_2_31_weight_elements_match_fp64():
+    """V = 2^19 + 5 rows of K = 4096: W, its packed copies and gW past 2^31 elements (64 chunks and
+    a partial one), 1000 tokens against the fp64 oracle."""
+    n, k, v, d = 1000, 4096, (1 << 19) + 5, 16
+    assert v * k > 2 ** 31
+    g = torch.Generator(device="cuda").manual_seed(2)
+    h = torch.randn(n, k, device="cuda", generator=g, dtype=torch.bfloat16)
+    W = (torch.randn(v, k, device="cuda", generator=g) * (3.0 / k ** 0.5)).bfloat16()
+    E = torch.randn(v, d, device="cuda", generator=g).bfloat16()
+    b = (0.5 * torch.randn(v, device="cuda", generator=g)).bfloat16()
+    gO = torch.randn(n, d, device="cuda", generator=g)
+    glse = 0.1 * torch.randn(n, device="cuda", generator=g)
+    xs = [x.requires_grad_(True) for x in (h, W, E, b)]
+    O, lse = swvr.softmax_readout(*xs)
+    grads = torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), xs)
+    got = (O.detach(), lse.detach(), *grads)
+    del xs, O, lse, grads
+    want = ref.reference_grads(h, W, E, b, gO, glse)
+    errs = {name: rel_err(a, r) for name, a, r in zip(("O", "lse", "gh", "gW", "gE", "gb"), got, want)}
+    print({key: f"{val:.1e}" for key, val in errs.items()}, flush=True)
+    assert errs["O"] <= 1e-2 and errs["lse"] <= 1e-2, errs
+    for name, a, r in zip(("gh", "gW", "gE", "gb"), got[2:], want[2:]):
+        assert errs[name] <= 2e-2, errs
+        assert cosine(a, r) >= 0.999, name
