@@ -271,3 +271,22 @@ def test_one_slice_stages_over_several_vocabulary_tiles(dtype, N, K, V, D):
     tol = 1e-5 if dtype == f32 else 1e-2
     assert rel_err(lse, lse_r) < tol / 10
     assert rel_err(O, O_r) < tol
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 4096), (torch.float32, 4000), (torch.bfloat16, 65536)])
+def test_embedding_widths_up_to_the_maximum(dtype, D):
+    """D far above one pass (the forward runs 256-column slices of E, fp32 128; the backward's wide
+    kernel streams D in 32-column slices, fp32 16), up to swvr_max_d = 65536, against the fp64
+    oracle: the north-star bar for bf16, fp32-sized for fp32."""
+    N, K, V = 300, 96, 700
+    h, W, E, b = make(N=N, K=K, V=V, D=D, dtype=dtype)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    gO = torch.randn(N, D, device="cuda", generator=g)
+    glse = torch.randn(N, device="cuda", generator=g)
+    O, lse = swvr.softmax_readout(h, W, E, b)
+    got = (O, lse, *torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), (h, W, E, b)))
+    want = ref.reference_grads(h, W, E, b, gO, glse)
+    lo = dtype != f32
+    for name, a, r in zip(("O", "lse", "gh", "gW", "gE", "gb"), got, want):
+        bar = (1e-2 if name in ("O", "lse") else 2e-2) if lo else 1e-5
+        assert rel_err(a, r) <= bar, (name, rel_err(a, r))
