@@ -290,3 +290,23 @@ def test_embedding_widths_up_to_the_maximum(dtype, D):
     for name, a, r in zip(("O", "lse", "gh", "gW", "gE", "gb"), got, want):
         bar = (1e-2 if name in ("O", "lse") else 2e-2) if lo else 1e-5
         assert rel_err(a, r) <= bar, (name, rel_err(a, r))
+
+
+@pytest.mark.parametrize("dtype,K", [(torch.bfloat16, 20007), (torch.float32, 9001)])
+def test_long_hidden_rows(dtype, K):
+    """K in the tens of thousands, not a multiple of the 32-element slice: the packed operands'
+    625 slices (fp32 16-element slices: 563) and the tail slice, against the fp64 oracle."""
+    N, V, D = 300, 700, 16
+    h, W, E, b = make(N=N, K=K, V=V, D=D, dtype=dtype)
+    with torch.no_grad():
+        W.mul_(K ** -0.5)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    gO = torch.randn(N, D, device="cuda", generator=g)
+    glse = torch.randn(N, device="cuda", generator=g)
+    O, lse = swvr.softmax_readout(h, W, E, b)
+    got = (O, lse, *torch.autograd.grad((O * gO).sum() + (lse * glse).sum(), (h, W, E, b)))
+    want = ref.reference_grads(h, W, E, b, gO, glse)
+    lo = dtype != f32
+    for name, a, r in zip(("O", "lse", "gh", "gW", "gE", "gb"), got, want):
+        bar = (1e-2 if name in ("O", "lse") else 2e-2) if lo else 1e-5
+        assert rel_err(a, r) <= bar, (name, rel_err(a, r))
