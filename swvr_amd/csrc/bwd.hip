@@ -933,6 +933,63 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   }
 }
 
+// ---------------------------------------------------------------- dE / db
+// gE and gb rows of a chunk from their partials, summed over the partials in a
+// fixed order (g ascending).  G_de: partials of dE ([G_de][DP][C]; 1 when the
+// gradient GEMM formed dE^T whole), G: partials of db ([G][C]).  One workgroup
+// of NT threads per tile of NT / 8 chunk rows x kRedD columns (kRedV for the
+// 256-thread kernel): the partial reads run along the rows (consecutive v, as
+// the partials store them), the sums pass through LDS, and gE is written along
+// its rows (consecutive d), so both sides coalesce.  The workgroups of column
+// tile 0 also write gb of their rows.
+constexpr int kRedV = 32, kRedD = 16;
+
+// sum_{g < n} p[g * stride] in order g = 0, 1, ...; the loads go out in batches of 8
+// ahead of their adds, so a long sum waits for memory once per batch, not once per term.
+__device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int g0 = 0; g0 < n; g0 += 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = g0 + u < n ? p[(int64_t)(g0 + u) * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (g0 + u < n) s += x[u];
+  }
+  return s;
+}
+
+// The dE / db rows of the tile at chunk row vb, column db0; tile: [NT / 8][kRedD + 1] floats of LDS.
+template <int NT>
+__device__ __forceinline__ void reduce_tile(float (*tile)[kRedD + 1], const float* __restrict__ part_dE,
+                                            const float* __restrict__ part_db, int G_de, int G, int C, int DP,
+                                            int v0, int cv, int D, void* gE, int gE_dtype, float* gb, int vb,
+                                            int db0) {
+  constexpr int RV = NT / 8;
+  const int t = threadIdx.x;
+  if (gE) {
+#pragma unroll
+    for (int j = 0; j < RV * kRedD / NT; ++j) {
+      const int i = j * NT + t;
+      const int dl = i / RV, vl = i % RV;  // consecutive threads: consecutive rows
+      const int v = vb + vl, d = db0 + dl;
+      tile[vl][dl] = v < cv && d < D ? ordered_sum(part_dE + (int64_t)d * C + v, (int64_t)DP * C, G_de) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < RV * kRedD / NT; ++j) {
+      const int i = j * NT + t;
+      const int vl = i / kRedD, dl = i % kRedD;  // consecutive threads: consecutive columns
+      const int v = vb + vl, d = db0 + dl;
+      if (v < cv && d < D) store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, tile[vl][dl]);
+    }
+  }
+  if (gb && db0 == 0 && t < RV) {
+    const int v = vb + t;
+    if (v < cv) gb[v0 + v] = ordered_sum(part_db + v, C, G);
+  }
+}
+
 // ---------------------------------------------------------------- GEMMs
 struct GemmParams {
   const void* stage;  // tiled dS (stage_off)
@@ -957,8 +1014,16 @@ struct GemmParams {
   const void* pstage;  // P, tiled like the dS stage
   const void* gOp;     // gO over positions [N_pad][DP]
   int DP;
-  float* part_dE;      // output dE^T [DP][C], fp32
+  float* part_dE;      // output dE^T [DP][C], fp32 (the scores kernels' dE partials when n_red > 0)
   int C;
+  // the chunk's dE / db reduction (reduce_tile), as n_red workgroups after the GEMM tiles, n_red_v of
+  // them along the chunk rows; n_red = 0 when the reduction is a launch of its own
+  int n_red, n_red_v;
+  const float* part_db;
+  int G_de, G_db, D;
+  void* gE;
+  int gE_dtype;
+  float* gb;
 };
 
 // Store 4 fp32 values as OutT (one 16- or 8-byte buffer store at byte offset
@@ -1291,6 +1356,18 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   static_assert(kStages * SB <= G::LDS_BYTES, "ring fits");
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
   int b = blockIdx.x;
+  {
+    // the dE / db reduction's workgroups follow every GEMM tile: the dispatcher reaches them last,
+    // and they run on the CUs the last round of tiles leaves idle
+    const int r = b - (p.n_dw + p.n_de + p.n_dh);
+    if (r >= 0) {
+      constexpr int RV = G::NT / 8;
+      reduce_tile<G::NT>(reinterpret_cast<float(*)[kRedD + 1]>(smem), p.part_dE, p.part_db, p.G_de, p.G_db, p.C,
+                         p.DP, p.v0, p.cv, p.D, p.gE, p.gE_dtype, p.gb, (r % p.n_red_v) * RV,
+                         (r / p.n_red_v) * kRedD);
+      return;
+    }
+  }
   if (b < p.n_dw) {
     int r, c;
     grouped_tile(b, p.n_dw / p.n_n, p.n_n, &r, &c);
@@ -1315,59 +1392,13 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   }
 }
 
-// ---------------------------------------------------------------- dE / db
-// gE and gb rows of a chunk from their partials, summed over the partials in a
-// fixed order (g ascending).  G_de: partials of dE ([G_de][DP][C]; 1 when the
-// gradient GEMM formed dE^T whole), G: partials of db ([G][C]).  One workgroup
-// per tile of kRedV chunk rows x kRedD columns: the partial reads run along the
-// rows (consecutive v, as the partials store them), the sums pass through LDS,
-// and gE is written along its rows (consecutive d), so both sides coalesce.  The
-// workgroups of column tile 0 also write gb of their rows.
-constexpr int kRedV = 32, kRedD = 16;
-
-// sum_{g < n} p[g * stride] in order g = 0, 1, ...; the loads go out in batches of 8
-// ahead of their adds, so a long sum waits for memory once per batch, not once per term.
-__device__ __forceinline__ float ordered_sum(const float* __restrict__ p, int64_t stride, int n) {
-  float s = 0.f;
-  for (int g0 = 0; g0 < n; g0 += 8) {
-    float x[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = g0 + u < n ? p[(int64_t)(g0 + u) * stride] : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (g0 + u < n) s += x[u];
-  }
-  return s;
-}
-
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict__ part_dE,
                                                          const float* __restrict__ part_db, int G_de, int G, int C,
                                                          int DP, int v0, int cv, int D, void* gE, int gE_dtype,
                                                          float* gb) {
   __shared__ float tile[kRedV][kRedD + 1];  // padded: the transposed accesses stay conflict-free
-  const int vb = blockIdx.x * kRedV, db0 = blockIdx.y * kRedD;
-  const int t = threadIdx.x;
-  if (gE) {
-#pragma unroll
-    for (int j = 0; j < kRedV * kRedD / 256; ++j) {
-      const int i = j * 256 + t;
-      const int dl = i / kRedV, vl = i % kRedV;  // consecutive threads: consecutive rows
-      const int v = vb + vl, d = db0 + dl;
-      tile[vl][dl] = v < cv && d < D ? ordered_sum(part_dE + (int64_t)d * C + v, (int64_t)DP * C, G_de) : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kRedV * kRedD / 256; ++j) {
-      const int i = j * 256 + t;
-      const int vl = i / kRedD, dl = i % kRedD;  // consecutive threads: consecutive columns
-      const int v = vb + vl, d = db0 + dl;
-      if (v < cv && d < D) store_as(gE, (int64_t)(v0 + v) * D + d, gE_dtype, tile[vl][dl]);
-    }
-  }
-  if (gb && blockIdx.y == 0 && t < kRedV) {
-    const int v = vb + t;
-    if (v < cv) gb[v0 + v] = ordered_sum(part_db + v, C, G);
-  }
+  reduce_tile<256>(tile, part_dE, part_db, G_de, G, C, DP, v0, cv, D, gE, gE_dtype, gb, blockIdx.x * kRedV,
+                   blockIdx.y * kRedD);
 }
 
 // Zero fill with a kernel (not hipMemsetAsync), so a caller may capture it in
@@ -1447,7 +1478,7 @@ hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStrea
 
 template <class T>
 hipError_t dispatch_gemm(const BwdPlan& plan, const GemmParams& gp, hipStream_t stream) {
-  const int blocks = gp.n_dw + gp.n_de + gp.n_dh;
+  const int blocks = gp.n_dw + gp.n_de + gp.n_dh + gp.n_red;
   if (blocks == 0) return hipSuccess;
   if (plan.GM != GemmTile<T>::GM || plan.GN != GemmTile<T>::GN) return hipErrorInvalidValue;
   timing_begin(kKindBwdGemm, stream);
@@ -1584,6 +1615,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if ((e = dispatch_scores<T>(plan, sp, stream)) != hipSuccess) return e;
 
     const bool gemm_de = pstage && p.gE;  // dE^T = gO^T P as tiles of the gradient GEMM launch
+    bool fold_red = false;
     if (need_stage || gemm_de) {
       GemmParams gp;
       gp.stage = stage;
@@ -1613,9 +1645,21 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.dh_first = c == 0;
       gp.scale = p.scale;
       gp.n_act = n_act;
+      // the reduction of the scores kernel's partials rides on this launch (the wide kernel's dE^T
+      // is formed in it, so that reduction follows as a launch of its own)
+      fold_red = (p.gE || p.gb) && !gemm_de;
+      gp.n_red_v = (cv + GemmTile<T>::NT / 8 - 1) / (GemmTile<T>::NT / 8);
+      gp.n_red = fold_red ? gp.n_red_v * (p.gE && p.D > 0 ? (p.D + kRedD - 1) / kRedD : 1) : 0;
+      gp.part_db = part_db;
+      gp.G_de = n_gpart_c;
+      gp.G_db = n_gpart_c;
+      gp.D = p.D;
+      gp.gE = p.gE;
+      gp.gE_dtype = p.gE_dtype;
+      gp.gb = p.gb;
       if ((e = dispatch_gemm<T>(plan, gp, stream)) != hipSuccess) return e;
     }
-    if (p.gE || p.gb) {
+    if ((p.gE || p.gb) && !fold_red) {
       timing_begin(kKindBwdReduce, stream);
       const dim3 grid((unsigned)((cv + kRedV - 1) / kRedV),
                       p.gE && p.D > 0 ? (unsigned)((p.D + kRedD - 1) / kRedD) : 1u);
