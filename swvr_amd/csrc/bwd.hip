@@ -3,14 +3,20 @@
 //   delta = rowsum(O * gO) - gLSE                                 bwd_delta_kernel
 //   per vocabulary chunk [v0, v0 + C):
 //     P  = exp(s * h W_c^T + b_c - LSE)        (scores recomputed)
-//     dS = P * (gO E_c^T - delta)                                 bwd_scores_kernel
+//     dS = P * (gO E_c^T - delta)                                 the scores kernels
 //       -> stage dS in the compute dtype, in 32 x 32 blocks (what the gradient GEMMs consume,
 //          swvr/chunked.py:143-145 / triton_kernels.py:108-109; the
 //          reference stages s*dS, here the GEMMs apply s to their outputs)
 //       -> dE_c = P^T gO and db_c = colsum(dS), accumulated per token group
 //          in registers and written as partials (no atomics)
 //     dW_c = s stage^T h   and   dh += s stage W_c                bwd_gemm_kernel
-//     dE_c, db_c = fixed-order sum of the partials                bwd_reduce_kernel
+//     dE_c, db_c = fixed-order sum of the partials                workgroups after the GEMM
+//                                                                 tiles of the same launch
+//                                                                 (bwd_reduce_kernel when
+//                                                                 neither gW nor gh is needed)
+//   Wide embeddings (bwd_scores_wide_kernel) keep no dE accumulator: the scores
+//   kernel also stages P, dE_c^T = gO^T P is a product of the GEMM launch, and
+//   bwd_reduce_kernel sums the db partials and writes gE from dE_c^T.
 // Every reduction has a fixed order, so gradients are bitwise reproducible.
 #include <type_traits>
 
