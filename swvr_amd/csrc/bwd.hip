@@ -14,6 +14,7 @@
 //                                                                 tiles of the same launch
 //                                                                 (bwd_reduce_kernel when
 //                                                                 neither gW nor gh is needed)
+//     W_{c+1} packed for the next scores launch                   workgroups after those
 //   Wide embeddings (bwd_scores_wide_kernel) keep no dE accumulator: the scores
 //   kernel also stages P, dE_c^T = gO^T P is a product of the GEMM launch, and
 //   bwd_reduce_kernel sums the db partials and writes gE from dE_c^T.
@@ -1030,6 +1031,15 @@ struct GemmParams {
   void* gE;
   int gE_dtype;
   float* gb;
+  // the packing of the next chunk's W rows for the scores kernel (pack_rows_tile), as n_pack
+  // workgroups after those, one 32-row x 8-slice tile per 256 threads at a time (n_pack_tiles in all)
+  int n_pack, n_pack_tiles;
+  const void* pk_src;  // W rows of the next chunk (fp32 when pk_f32, else the compute dtype)
+  int pk_f32;
+  int64_t pk_ld;
+  int pk_rows, pk_S;
+  void* pk_dst;        // their packed image
+  void* pk_rowmajor;   // and the row-major copy in the compute dtype (fp32 W), or null
 };
 
 // Store 4 fp32 values as OutT (one 16- or 8-byte buffer store at byte offset
@@ -1349,6 +1359,32 @@ __device__ __forceinline__ void gemm_tile_de(const GemmParams& p, int t, char* s
   gemm_store<G>(acc, 1.f, p.part_dE, nullptr, 0, p.DP, mt * GM, nt * GN, p.C, smem);
 }
 
+// Workgroup w of the W packing riding on a GEMM launch: tiles H i + part for i = w, w + n_pack, ...,
+// each 256-thread part (H = NT / 256 of them) packing one tile through its own LDS block.
+template <class T, int NT>
+__device__ __forceinline__ void gemm_pack_w(const GemmParams& p, int w, char* smem) {
+  constexpr int H = NT / 256;
+  static_assert(NT % 256 == 0, "whole 256-thread parts");
+  const int part = (int)threadIdx.x >> 8, t = (int)threadIdx.x & 255;
+  uint4* tile = reinterpret_cast<uint4*>(smem) + part * (32 * 33);
+  const int K = p.K;
+  for (int i = w; H * i < p.n_pack_tiles; i += p.n_pack) {
+    const int ti = H * i + part;
+    const int grp_s = ti < p.n_pack_tiles ? ti : -1;
+    if constexpr (sizeof(T) == 2) {
+      if (p.pk_f32) {
+        pack_rows_tile<float, T>(grp_s, t, tile, static_cast<const float*>(p.pk_src), p.pk_ld, p.pk_rows, K, p.pk_S,
+                                 static_cast<T*>(p.pk_dst), static_cast<T*>(p.pk_rowmajor), nullptr, nullptr);
+        __syncthreads();  // the next pair of tiles reuses the LDS blocks
+        continue;
+      }
+    }
+    pack_rows_tile<T, T>(grp_s, t, tile, static_cast<const T*>(p.pk_src), p.pk_ld, p.pk_rows, K, p.pk_S,
+                         static_cast<T*>(p.pk_dst), nullptr, nullptr, nullptr);
+    __syncthreads();  // the next pair of tiles reuses the LDS blocks
+  }
+}
+
 // One launch covers the gradient products of a chunk: blocks [0, n_dw) are
 // dW tiles, then n_de dE^T tiles (wide scores kernel only), then dh tiles.
 // The dW and dE^T tiles (reductions over all active positions) are dealt first.
@@ -1363,14 +1399,19 @@ __global__ __launch_bounds__(GemmTile<T>::NT) void bwd_gemm_kernel(GemmParams p)
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
   int b = blockIdx.x;
   {
-    // the dE / db reduction's workgroups follow every GEMM tile: the dispatcher reaches them last,
-    // and they run on the CUs the last round of tiles leaves idle
+    // the dE / db reduction's workgroups, then the next chunk's W packing, follow every GEMM
+    // tile: the dispatcher reaches them last, and they run on the CUs the last round of tiles
+    // leaves idle
     const int r = b - (p.n_dw + p.n_de + p.n_dh);
-    if (r >= 0) {
+    if (r >= 0 && r < p.n_red) {
       constexpr int RV = G::NT / 8;
       reduce_tile<G::NT>(reinterpret_cast<float(*)[kRedD + 1]>(smem), p.part_dE, p.part_db, p.G_de, p.G_db, p.C,
                          p.DP, p.v0, p.cv, p.D, p.gE, p.gE_dtype, p.gb, (r % p.n_red_v) * RV,
                          (r / p.n_red_v) * kRedD);
+      return;
+    }
+    if (r >= p.n_red) {
+      gemm_pack_w<T, G::NT>(p, r - p.n_red, smem);
       return;
     }
   }
@@ -1484,7 +1525,7 @@ hipError_t dispatch_scores(const BwdPlan& plan, const ScoresParams& sp, hipStrea
 
 template <class T>
 hipError_t dispatch_gemm(const BwdPlan& plan, const GemmParams& gp, hipStream_t stream) {
-  const int blocks = gp.n_dw + gp.n_de + gp.n_dh + gp.n_red;
+  const int blocks = gp.n_dw + gp.n_de + gp.n_dh + gp.n_red + gp.n_pack;
   if (blocks == 0) return hipSuccess;
   if (plan.GM != GemmTile<T>::GM || plan.GN != GemmTile<T>::GN) return hipErrorInvalidValue;
   timing_begin(kKindBwdGemm, stream);
@@ -1523,6 +1564,10 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   const bool f8 = p.hq != nullptr;
   T* hqc = reinterpret_cast<T*>(ws + plan.off_hqc);
   float* multp = f8 ? reinterpret_cast<float*>(ws + plan.off_mult) : nullptr;
+  const bool need_stage = p.gh || p.gW;
+  const bool gemm_de = pstage && p.gE;  // dE^T = gO^T P as tiles of the gradient GEMM launch
+  // every chunk has a gradient GEMM launch: the W packing of the scores kernel rides on them
+  const bool fold_pack = !f8 && (need_stage || gemm_de);
 
   {
     // delta, the active tokens, and the token-side operands over positions
@@ -1567,14 +1612,17 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     } else {
       if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
         return e;
-      // fp32 W: the packing also writes the row-major copy the dh product reads
-      if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, p.V, p.K, plan.hS, plan.V_pad, Wp, stream, Wc)) != hipSuccess)
+      // fp32 W: the packing also writes the row-major copy the dh product reads.  When every
+      // chunk has a gradient GEMM launch, chunk c + 1's rows are packed by chunk c's launch
+      // (gemm_pack_w), so only the first chunk's are packed here.
+      const int64_t rows0 = fold_pack ? (p.V < plan.C ? p.V : plan.C) : p.V;
+      const int64_t pad0 = fold_pack ? (rows0 + plan.BV - 1) / plan.BV * plan.BV : plan.V_pad;
+      if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, (int)rows0, p.K, plan.hS, pad0, Wp, stream, Wc)) != hipSuccess)
         return e;
     }
     timing_end(kKindPack, stream);
   }
 
-  const bool need_stage = p.gh || p.gW;
   for (int c = 0; c < plan.n_chunks; ++c) {
     const int v0 = (int)(c * plan.C);
     const int cv = (int)((p.V - v0) < plan.C ? (p.V - v0) : plan.C);
@@ -1620,7 +1668,6 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     sp.DP = plan.DP;
     if ((e = dispatch_scores<T>(plan, sp, stream)) != hipSuccess) return e;
 
-    const bool gemm_de = pstage && p.gE;  // dE^T = gO^T P as tiles of the gradient GEMM launch
     bool fold_red = false;
     if (need_stage || gemm_de) {
       GemmParams gp;
@@ -1663,6 +1710,26 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.gE = p.gE;
       gp.gE_dtype = p.gE_dtype;
       gp.gb = p.gb;
+      // the next chunk's W rows into the scores kernel's packed image (and the row-major copy of
+      // an fp32 W), as in the packing before the loop
+      gp.n_pack = gp.n_pack_tiles = 0;
+      if (fold_pack && c + 1 < plan.n_chunks) {
+        const int64_t v1 = v0 + plan.C;
+        const int cv1 = (int)((p.V - v1) < plan.C ? (p.V - v1) : plan.C);
+        const int pad1 = (cv1 + plan.BV - 1) / plan.BV * plan.BV;
+        constexpr int H = GemmTile<T>::NT / 256;
+        const bool f32src = sizeof(T) == 2 && p.w_f32;
+        gp.pk_f32 = f32src;
+        gp.pk_src = static_cast<const char*>(p.W) + v1 * p.ldw * (f32src ? 4 : (int64_t)sizeof(T));
+        gp.pk_ld = p.ldw;
+        gp.pk_rows = cv1;
+        gp.pk_S = plan.hS;
+        gp.pk_dst = Wp + v1 * plan.hS * SliceK<T>::value;
+        gp.pk_rowmajor = Wc ? Wc + v1 * p.K : nullptr;
+        gp.n_pack_tiles = (pad1 / 32) * ((plan.hS + 7) / 8);
+        const int iters = (gp.n_pack_tiles + H - 1) / H;
+        gp.n_pack = iters < 1024 ? iters : 1024;
+      }
       if ((e = dispatch_gemm<T>(plan, gp, stream)) != hipSuccess) return e;
     }
     if ((p.gE || p.gb) && !fold_red) {

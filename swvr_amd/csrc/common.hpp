@@ -924,21 +924,24 @@ __device__ __forceinline__ bool chunk_nonfinite(uint4 v) {
 // selected tokens in position order).  With nonfinite set, a workgroup that
 // packs an infinity or a NaN stores 1 there (every such store writes the same
 // value, so the word ends as 1 whatever their order).
+// One 32-row x 8-slice tile `grp_s` (32-row group grp_s / SG, slices from (grp_s % SG) * 8)
+// of pack_rows_tiled_kernel, by 256 threads (t = 0..255) through `tile` (32 x 33 chunks of
+// LDS).  Every thread of the workgroup takes part in the barriers; a caller whose
+// threads share a workgroup among several tiles passes grp_s < 0 for threads with no
+// tile, which then only keep the barriers.  Returns whether this thread packed a
+// non-finite value.
 template <class Src, class T>
-__global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restrict__ src, int64_t ld, int N, int K,
-                                                              int S, T* __restrict__ dst, T* __restrict__ rowmajor,
-                                                              const int* __restrict__ rows,
-                                                              const int* __restrict__ n_rows,
-                                                              int* __restrict__ nonfinite) {
+__device__ __forceinline__ bool pack_rows_tile(int grp_s, int t, uint4* tile, const Src* __restrict__ src, int64_t ld,
+                                               int N, int K, int S, T* __restrict__ dst, T* __restrict__ rowmajor,
+                                               const int* __restrict__ rows, const int* __restrict__ n_rows) {
   constexpr int BK = SliceK<T>::value, CE = 16 / (int)sizeof(T), CPR = BK / CE;
   static_assert(CPR == 4, "4 chunks per slice row");
-  constexpr int SPW = 8;                    // slices per workgroup
+  constexpr int SPW = 8;                    // slices per tile
   constexpr int RSTRIDE = SPW * CPR + 1;    // chunks per LDS row (one pad chunk: no bank conflicts)
-  __shared__ uint4 tile[32 * RSTRIDE];
   const int SG = (S + SPW - 1) / SPW;
-  const int grp = blockIdx.x / SG, s0 = (blockIdx.x % SG) * SPW;
-  const int ns = S - s0 < SPW ? S - s0 : SPW;
-  const int t = threadIdx.x;
+  const bool live = grp_s >= 0;
+  const int grp = live ? grp_s / SG : 0, s0 = live ? (grp_s % SG) * SPW : 0;
+  const int ns = !live ? 0 : S - s0 < SPW ? S - s0 : SPW;
   const int nr = rows ? n_rows[0] : N;
   bool bad = false;
 #pragma unroll
@@ -955,7 +958,6 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restr
     }
     tile[row * RSTRIDE + kc] = v;
   }
-  if (nonfinite && __syncthreads_or(bad) && t == 0) nonfinite[0] = 1;
   __syncthreads();
   T* out = dst + ((int64_t)grp * S + s0) * 32 * BK;
 #pragma unroll
@@ -965,6 +967,19 @@ __global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restr
     if (sl < ns)
       reinterpret_cast<uint4*>(out)[o] = tile[r * RSTRIDE + sl * CPR + (pc ^ chunk_swizzle(r, CPR))];
   }
+  return bad;
+}
+
+template <class Src, class T>
+__global__ __launch_bounds__(256) void pack_rows_tiled_kernel(const Src* __restrict__ src, int64_t ld, int N, int K,
+                                                              int S, T* __restrict__ dst, T* __restrict__ rowmajor,
+                                                              const int* __restrict__ rows,
+                                                              const int* __restrict__ n_rows,
+                                                              int* __restrict__ nonfinite) {
+  __shared__ uint4 tile[32 * 33];
+  const bool bad = pack_rows_tile<Src, T>((int)blockIdx.x, (int)threadIdx.x, tile, src, ld, N, K, S, dst, rowmajor,
+                                          rows, n_rows);
+  if (nonfinite && __syncthreads_or(bad) && threadIdx.x == 0) nonfinite[0] = 1;
 }
 
 // Pack rows [rows_pad][K] of src (rows_pad a multiple of 32) into the tile image.
