@@ -9,7 +9,13 @@
 //   2  random operands read from LDS every step, 6 x 16-byte reads per 8
 //      MFMAs, as the forward / gradient GEMM loops read them;
 //   3, 4  the same with 4 and 3 reads per 8 MFMAs (the read rate of larger
-//      wave tiles), which shows how much the LDS read rate costs.
+//      wave tiles), which shows how much the LDS read rate costs;
+//   5  as 2 in the hot loops' order: the next step's operands read under the
+//      current step's MFMAs (mma_load_step), so no MFMA waits on its own reads;
+//   6  the A operands from LDS (4 reads per 8 MFMAs) and the B operands loaded
+//      from a 2 MB device array (L2-resident) straight into registers, 8 steps
+//      ahead: an operand path that bypasses LDS (iters rounded up to a multiple
+//      of 8).
 // Comparing the rates shows how much of the datasheet peak this chip reaches
 // with the operand data and LDS traffic of the real kernels, i.e. the ceiling
 // that power and clock set for them.
@@ -38,7 +44,17 @@ __device__ __forceinline__ bf16_t random_bf16(uint32_t h) {
   return v;
 }
 
-__global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, int mode, uint32_t seed, float* out) {
+// Mode 6's register-fed operands: 2 MB of random bf16, filled before the timed launches.
+constexpr int kProbeSrc = 1 << 20;  // elements
+__device__ bf16_t g_probe_src[kProbeSrc];
+
+__global__ __launch_bounds__(256) void probe_fill_kernel(uint32_t seed) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < kProbeSrc; i += gridDim.x * 256)
+    g_probe_src[i] = random_bf16(mix32(seed ^ (uint32_t)i * 2654435761u));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t seed, float* out) {
   __shared__ __attribute__((aligned(1024))) bf16_t lds[16384];  // 32 KB of operands
   const int tid = threadIdx.x, lane = lane_id();
   const uint32_t base = mix32(seed ^ (blockIdx.x * 512u + tid));
@@ -48,11 +64,11 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, int mode, ui
 #pragma unroll
   for (int f = 0; f < 4; ++f)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) a[f][t] = mode == 1 ? (bf16_t)0.f : random_bf16(mix32(base + 8 * f + t));
+    for (int t = 0; t < 8; ++t) a[f][t] = MODE == 1 ? (bf16_t)0.f : random_bf16(mix32(base + 8 * f + t));
 #pragma unroll
   for (int f = 0; f < 2; ++f)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) b[f][t] = mode == 1 ? (bf16_t)0.f : random_bf16(mix32(base + 64 + 8 * f + t));
+    for (int t = 0; t < 8; ++t) b[f][t] = MODE == 1 ? (bf16_t)0.f : random_bf16(mix32(base + 64 + 8 * f + t));
   f32x16_t acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -60,20 +76,70 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, int mode, ui
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
   const char* lb = reinterpret_cast<const char*>(lds);
   const int wb = wave_id() * 1024;
-  for (int it = 0; it < iters; ++it) {
-    if (mode >= 2) {
+  if constexpr (MODE == 5) {
+    // the hot loops' order: B operands of the next step first, then each A operand after the
+    // last MFMA of the current step that uses its predecessor
+    bf16x8_t na[4], nb[2];
+    for (int it = 0; it < iters; ++it) {
+      const char* win = lb + ((it + 1) & 3) * 8192 + lane * 16;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) nb[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mfma_k16(acc[i][j], a[i], b[j]);
+        na[i] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + i * 1024) & 8191));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int f = 0; f < 4; ++f) a[f] = na[f];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) b[f] = nb[f];
+    }
+  } else if constexpr (MODE == 6) {
+    // B from the device array, 8 steps ahead: step s reads 2 KB at (wave base + 2 KB s) mod 2 MB
+    constexpr int Q = 8;
+    const char* src = reinterpret_cast<const char*>(g_probe_src);
+    const uint32_t base = (uint32_t)(blockIdx.x * 8 + wave_id()) * 65536u;
+    auto goff = [&](int step, int f) {
+      return (base + (uint32_t)step * 2048u + (uint32_t)f * 1024u + (uint32_t)lane * 16u) & (2u * kProbeSrc - 1u);
+    };
+    bf16x8_t q[Q][2];
+#pragma unroll
+    for (int s = 0; s < Q; ++s)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) q[s][f] = *reinterpret_cast<const bf16x8_t*>(src + goff(s, f));
+    for (int it = 0; it < iters; it += Q) {
+#pragma unroll
+      for (int s = 0; s < Q; ++s) {
+        const char* win = lb + ((it + s) & 3) * 8192 + lane * 16;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) a[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + f * 1024) & 8191));
+        b[0] = q[s][0];
+        b[1] = q[s][1];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) q[s][f] = *reinterpret_cast<const bf16x8_t*>(src + goff(it + s + Q, f));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) mfma_k16(acc[i][j], a[i], b[j]);
+      }
+    }
+  }
+  for (int it = 0; it < (MODE >= 5 ? 0 : iters); ++it) {
+    if constexpr (MODE >= 2) {
       // 16-byte operand reads per step, one 1 KB wave-wide piece each, from the
-      // 8 KB window (it % 4) of the 32 KB: offsets stay below 4 * 8192.  mode 2 reads
+      // 8 KB window (it % 4) of the 32 KB: offsets stay below 4 * 8192.  MODE 2 reads
       // all six operands (a 128 x 64 wave tile), 3 four (the operand count per MFMA of
       // a 128 x 128 tile), 4 three
       const char* win = lb + (it & 3) * 8192 + lane * 16;
-      const int na = mode == 2 ? 4 : mode == 3 ? 3 : 2;
+      const int na = MODE == 2 ? 4 : MODE == 3 ? 3 : 2;
 #pragma unroll
       for (int f = 0; f < 4; ++f)
         if (f < na) a[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + f * 1024) & 8191));
 #pragma unroll
       for (int f = 0; f < 2; ++f)
-        if (mode == 2 || f == 0) b[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
+        if (MODE == 2 || f == 0) b[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -93,8 +159,22 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, int mode, ui
 }  // namespace
 
 hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream_t stream) {
+  if (mode == 6) {
+    probe_fill_kernel<<<256, 256, 0, stream>>>(0x5eedu);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   timing_begin(kKindProbe, stream);
-  probe_mfma_kernel<<<workgroups, 512, 0, stream>>>(iters, mode, 0x5eedu, out);
+  switch (mode) {
+    case 0: probe_mfma_kernel<0><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 1: probe_mfma_kernel<1><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 2: probe_mfma_kernel<2><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 3: probe_mfma_kernel<3><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 4: probe_mfma_kernel<4><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 5: probe_mfma_kernel<5><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 6: probe_mfma_kernel<6><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    default: return hipErrorInvalidValue;
+  }
   timing_end(kKindProbe, stream);
   return hipGetLastError();
 }
