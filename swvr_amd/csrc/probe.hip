@@ -15,7 +15,12 @@
 //   6  the A operands from LDS (4 reads per 8 MFMAs) and the B operands loaded
 //      from a 2 MB device array (L2-resident) straight into registers, 8 steps
 //      ahead: an operand path that bypasses LDS (iters rounded up to a multiple
-//      of 8).
+//      of 8);
+//   7  the hot loops' whole step: mode 5 plus a workgroup barrier every 2 steps
+//      and, per 2 steps, 32 KB of direct-to-LDS stage loads (buffer_load ...
+//      lds) from the 2 MB array into a 3-slot ring, waited for as the loops
+//      wait (the stage traffic every LDS-fed loop here carries; iters rounded
+//      up to a multiple of 2).
 // Comparing the rates shows how much of the datasheet peak this chip reaches
 // with the operand data and LDS traffic of the real kernels, i.e. the ceiling
 // that power and clock set for them.
@@ -55,7 +60,8 @@ __global__ __launch_bounds__(256) void probe_fill_kernel(uint32_t seed) {
 
 template <int MODE>
 __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t seed, float* out) {
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[16384];  // 32 KB of operands
+  // 32 KB of operands (and, mode 7, a 3-slot ring of 32 KB stages after them)
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[16384 + (MODE == 7 ? 3 * 16384 : 0)];
   const int tid = threadIdx.x, lane = lane_id();
   const uint32_t base = mix32(seed ^ (blockIdx.x * 512u + tid));
   for (int i = tid; i < 16384; i += 512) lds[i] = random_bf16(mix32(seed * 31u + i));
@@ -76,7 +82,50 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t see
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
   const char* lb = reinterpret_cast<const char*>(lds);
   const int wb = wave_id() * 1024;
-  if constexpr (MODE == 5) {
+  if constexpr (MODE == 7) {
+    // stage s (every 2 steps) = 4 loads per thread of 16 bytes from the array into slot s % 3,
+    // issued 2 stages ahead; before the barrier that ends a stage the next one has landed
+    const rsrc_t rs = make_rsrc(g_probe_src);
+    const uint32_t ring = lds_addr(lds + 16384);
+    auto stage_load = [&](int st) {
+      const uint32_t slot = ring + (uint32_t)(st % 3) * 32768u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma_batch1(rs, ((uint32_t)st * 32768u + (uint32_t)i * 8192u + (uint32_t)threadIdx.x * 16u) &
+                           (2u * kProbeSrc - 1u),
+                   slot + (uint32_t)i * 8192u + (uint32_t)wave_id() * 1024u);
+    };
+    stage_load(0);
+    stage_load(1);
+    bf16x8_t na[4], nb[2];
+    for (int it = 0; it < iters; it += 2) {
+      stage_load(it / 2 + 2);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const char* win = lb + ((it + s2 + 1) & 3) * 8192 + lane * 16;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) nb[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) mfma_k16(acc[i][j], a[i], b[j]);
+          na[i] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + i * 1024) & 8191));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (s2 == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<4>();  // the next stage has landed; the one after it may stay in flight
+          stage_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int f = 0; f < 4; ++f) a[f] = na[f];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) b[f] = nb[f];
+      }
+    }
+    wait_vmcnt<0>();  // no stage load outstanding when the workgroup ends
+  } else if constexpr (MODE == 5) {
     // the hot loops' order: B operands of the next step first, then each A operand after the
     // last MFMA of the current step that uses its predecessor
     bf16x8_t na[4], nb[2];
@@ -159,7 +208,7 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t see
 }  // namespace
 
 hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream_t stream) {
-  if (mode == 6) {
+  if (mode == 6 || mode == 7) {
     probe_fill_kernel<<<256, 256, 0, stream>>>(0x5eedu);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -173,6 +222,7 @@ hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream
     case 4: probe_mfma_kernel<4><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     case 5: probe_mfma_kernel<5><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     case 6: probe_mfma_kernel<6><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 7: probe_mfma_kernel<7><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     default: return hipErrorInvalidValue;
   }
   timing_end(kKindProbe, stream);
