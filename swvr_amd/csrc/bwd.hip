@@ -47,7 +47,13 @@ __device__ __forceinline__ void store_as(void* base, int64_t idx, int dtype, flo
 // positions 0 .. n_act - 1; positions n_act .. N_pad - 1 are padding.
 
 // delta = rowsum(O * gO) - gLSE (swvr/chunked.py:113-114) and the active flag,
-// one thread per token.
+// one thread per token.  gO enters the sum rounded to the compute dtype T, as it
+// enters dP = gO E^T: the reference sums it unrounded, which leaves dP - delta,
+// where those nearly cancel (one vocabulary row, or one row with all of P),
+// with the rounding error of gO alone (gh and gb then miss the fp32 formula by
+// 2-7% in bf16 at V = 1, D = 300; 0.2% with the rounded sum).  Elsewhere the two
+// sums agree to that rounding.
+template <class T>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(const float* __restrict__ O, const float* __restrict__ gO,
                                                         const float* __restrict__ glse, int N, int D,
                                                         float* __restrict__ delta, int* __restrict__ flag) {
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const float* __restrict_
   bool nz = false;
   for (int k = 0; k < D; ++k) {
     const float g = gO[(int64_t)n * D + k];
-    s += O[(int64_t)n * D + k] * g;
+    s += O[(int64_t)n * D + k] * to_float(from_float<T>(g));
     nz |= g != 0.f;
   }
   s -= glse[n];
@@ -1572,7 +1578,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   {
     // delta, the active tokens, and the token-side operands over positions
     timing_begin(kKindBwdDelta, stream);
-    bwd_delta_kernel<<<(p.N + 255) / 256, 256, 0, stream>>>(p.O, p.gO, p.glse, p.N, p.D, delta, flag);
+    bwd_delta_kernel<T><<<(p.N + 255) / 256, 256, 0, stream>>>(p.O, p.gO, p.glse, p.N, p.D, delta, flag);
     bwd_compact_kernel<<<1, 1024, 0, stream>>>(flag, p.N, idx, inv, n_act);
     const int64_t n = (int64_t)plan.N_pad * plan.DP;
     bwd_pack_kernel<T><<<(int)((n + 255) / 256), 256, 0, stream>>>(p.gO, p.lse, delta, idx, n_act, p.D,
