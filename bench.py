@@ -1,6 +1,6 @@
 """Benchmark: fwd+bwd of swvr_amd.softmax_readout_mse on one MI355X.
 
-    python bench.py                      # headline (config 3), 10 timed steps
+    python bench.py                      # headline (config 3), 150 timed steps (about 6 s of GPU work)
     python bench.py --config 2 --steps 20 --warmup 3
     python bench.py --no-cpu             # skip the CPU baseline leg
     python bench.py --copy-probe-mib 1024  # only a plain device copy (HBM counter calibration)
@@ -373,8 +373,8 @@ def fp8_path(h, W, E, b, target, weight, z, chunk, params, fwd_flops, flops, ite
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=150)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--chunk", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
