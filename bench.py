@@ -135,7 +135,8 @@ def load_traffic():
 
 
 def measured_traffic(t, config, kernel):
-    """Calibrated HBM (fetch, write) bytes per launch of ``kernel`` at ``config``, or None."""
+    """Calibrated L2-miss (fetch, write) bytes per launch of ``kernel`` at ``config``, or None
+    (fabric bytes: Infinity Cache hits included)."""
     try:
         e = t["configs"][str(config)][kernel]
     except (TypeError, KeyError):
@@ -189,8 +190,10 @@ def traffic_summary(root):
     cw, _ = per_kernel("copy_write", "WRITE_SIZE")
     copy_f = max(cf.values()) if cf else None
     copy_w = max(cw.values()) if cw else None
-    out = {"about": "HBM bytes per dispatch of the streaming kernels: rocprofv3 FETCH_SIZE and WRITE_SIZE (KiB per "
-                    "dispatch, averaged) scaled by what the same counters read for a plain 1 GiB copy; "
+    out = {"about": "L2-miss (fabric) bytes per dispatch of the streaming kernels: rocprofv3 FETCH_SIZE and "
+                    "WRITE_SIZE (KiB per dispatch, averaged; they count the L2's requests to the fabric, Infinity "
+                    "Cache hits included, so they bound DRAM traffic from above) scaled by what the same counters "
+                    "read for a plain 1 GiB copy, which misses the 256 MB Infinity Cache; "
                     "bytes = fetch_kib * 1024 * fetch_scale + write_kib * 1024 * write_scale. "
                     "source_sha: the HIP sources measured (bench.py source_sha).",
            "source_sha": source_sha(),
@@ -289,22 +292,81 @@ def mfma_probe(iters=1 << 20, launches=3):
 
 
 def library_gemm(cfg, chunk, reps=10):
-    """Calibration of the gradient GEMMs against the vendor library: torch.mm (hipBLASLt on ROCm)
-    on one chunk's two products at this configuration's shape, dW_c = dS_c^T h (C x Q)(Q x K) and
-    dh = dS_c W_c (Q x C)(C x K) with fp32 and bf16 outputs, Q = the bench's active tokens rounded
-    to 32 as the library's GEMM runs them, N(0,1) bf16 operands.  Measurement only: the product's
-    gradient GEMMs are this repository's own kernel (bwd_gemm_kernel), which forms both in one launch."""
-    g = torch.Generator(device="cuda").manual_seed(0)
-    _, _, _, _, _, weight, _ = make_inputs(cfg, "cuda")
-    n_act = int((weight != 0).sum().item()) if weight is not None else cfg["N"]
-    Q, C, K = (n_act + 31) // 32 * 32, min(chunk, cfg["V"]), cfg["K"]
-    r = lambda *s: torch.randn(*s, device="cuda", generator=g).to(torch.bfloat16)
-    S, h, Wc = r(C, Q), r(Q, K), r(C, K)
-    St = S.t().contiguous()
+    """Calibration of the gradient GEMMs against the vendor library (hipBLASLt through torch.mm) on
+    one vocabulary chunk of this configuration: W, E and bias cut to their first ``chunk`` rows, so
+    that the whole backward is one chunk.
+
+    * ``real_ds``: the library on the dS our kernel consumes.  The same one-chunk problem runs
+      through swvr_amd (the MSE loss with the config's weight and z-loss, forward and backward, its
+      launches timed); torch recomputes that chunk's dS over the active tokens from swvr_amd's O
+      and lse (S in fp32, P = exp(S + b - lse), dP from gO rounded to bf16, dS rounded to bf16) and
+      times dW_c = dS^T h (C x Q)(Q x K, bf16 out) and dh = dS W_c (Q x C)(C x K, fp32 out).  Operand
+      values set the chip's power and clock, so only identical operands compare kernels.
+      ``bwd_gemm_kernel`` forms both products in one launch (dh read-modify-written in fp32) and
+      the chunk's dE / db reduction after its tiles.
+    * ``normal_operands``: the library on N(0,1) bf16 operands of the same shapes (the earlier
+      calibration).
+    Measurement only: the product's gradient GEMMs are this repository's own kernel."""
+    import swvr_amd as swvr
+    from swvr_amd import _lib
+    dev = torch.device("cuda")
+    h, W, E, b, target, weight, _ = make_inputs(cfg, dev)
+    N, K, D = cfg["N"], cfg["K"], cfg["D"]
+    h = h.detach().reshape(-1, K)
+    target = target.reshape(-1, D)
+    weight = weight.reshape(-1) if weight is not None else None
+    C = min(chunk, cfg["V"])
+    Wc = W.detach()[:C].clone().requires_grad_(True)
+    Ec = E.detach()[:C].clone().requires_grad_(True)
+    bc = b.detach()[:C].clone().requires_grad_(True) if b is not None else None
+    hl = h.clone().requires_grad_(True)
+    z = cfg["z"]
+
+    def ours():
+        for x in (hl, Wc, Ec, bc):
+            if x is not None:
+                x.grad = None
+        swvr.softmax_readout_mse(hl, Wc, Ec, target, bc, weight=weight, z_loss_weight=z, chunk_size=C).backward()
+
+    ours()
+    torch.cuda.synchronize()
+    _lib.kernel_timing(True)
+    _lib.kernel_timing(None)
+    for _ in range(reps):
+        ours()
+    torch.cuda.synchronize()
+    k = _lib.kernel_timing(None)
+    _lib.kernel_timing(False)
+    gemm_ms = k["bwd_gemm_kernel"][0] / k["bwd_gemm_kernel"][1]
+
+    with torch.no_grad():
+        O, lse = swvr.softmax_readout(h, Wc.detach(), Ec.detach(), bc.detach() if bc is not None else None,
+                                      chunk_size=C)
+        w = weight if weight is not None else torch.ones(N, device=dev)
+        den = w.sum()
+        gO = 2.0 * (O - target) * (w / (D * den))[:, None]
+        glse = 2.0 * z * lse * w / den
+        rows = torch.nonzero(w != 0).flatten()
+        n_act = rows.numel()
+        Q = (n_act + 31) // 32 * 32
+        hA = torch.zeros(Q, K, dtype=torch.bfloat16, device=dev)
+        hA[:n_act] = h[rows]
+        gOA = gO[rows].to(torch.bfloat16).float()
+        S = hA[:n_act].float() @ Wc.detach().float().t()
+        if bc is not None:
+            S += bc.detach().float()[None, :]
+        P = torch.exp(S - lse[rows][:, None])
+        del S
+        dP = gOA @ Ec.detach().float().t()
+        delta = (O[rows] * gOA).sum(1) - glse[rows]
+        dS = torch.zeros(Q, C, dtype=torch.bfloat16, device=dev)
+        dS[:n_act] = (P * (dP - delta[:, None])).to(torch.bfloat16)
+        del P, dP
+        dSt = dS.t().contiguous()
+        Wcb = Wc.detach().contiguous()
     flops = 2.0 * C * Q * K
-    res = {"shape": {"C": C, "Q": Q, "K": K}}
-    for name, fn in (("dW_bf16_out", lambda: torch.mm(S, h)), ("dh_bf16_out", lambda: torch.mm(St, Wc)),
-                     ("dh_fp32_out", lambda: torch.mm(St, Wc, out_dtype=torch.float32))):
+
+    def timed(fn):
         fn()
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -314,8 +376,23 @@ def library_gemm(cfg, chunk, reps=10):
         t1.record()
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / reps
-        res[name] = {"ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
-    return res
+        return {"ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+    real = {"dW_bf16_out": timed(lambda: torch.mm(dSt, hA)),
+            "dh_fp32_out": timed(lambda: torch.mm(dS, Wcb, out_dtype=torch.float32))}
+    lib_ms = real["dW_bf16_out"]["ms"] + real["dh_fp32_out"]["ms"]
+    real["library_pair_ms"] = round(lib_ms, 3)
+    real["library_pair_tflops"] = round(2 * flops / (lib_ms * 1e-3) / 1e12, 1)
+    real["bwd_gemm_kernel_ms"] = round(gemm_ms, 3)
+    real["bwd_gemm_kernel_tflops"] = round(2 * flops / (gemm_ms * 1e-3) / 1e12, 1)
+    real["ds_abs_mean"] = float(dS.float().abs().mean())
+    g = torch.Generator(device="cuda").manual_seed(0)
+    r = lambda *s: torch.randn(*s, device="cuda", generator=g).to(torch.bfloat16)
+    Sn, hn, Wn = r(C, Q), r(Q, K), r(C, K)
+    Snt = Sn.t().contiguous()
+    normal = {"dW_bf16_out": timed(lambda: torch.mm(Sn, hn)), "dh_bf16_out": timed(lambda: torch.mm(Snt, Wn)),
+              "dh_fp32_out": timed(lambda: torch.mm(Snt, Wn, out_dtype=torch.float32))}
+    return {"shape": {"C": C, "Q": Q, "K": K, "active_tokens": n_act}, "real_ds": real, "normal_operands": normal}
 
 
 def fp8_path(h, W, E, b, target, weight, z, chunk, params, fwd_flops, flops, iters):
@@ -381,7 +458,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device-to-device copy of this many MiB, 5 times, and exit: "
-                         "its FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc calibrate the HBM traffic counters")
+                         "its FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc calibrate the L2-miss (fabric) traffic counters")
     ap.add_argument("--no-fp8", action="store_true", help="skip the opt-in e4m3 leg")
     ap.add_argument("--traffic-from", default=None,
                     help="print the traffic summary (profiles/readout_traffic.json) built from rocprofv3 "
@@ -467,6 +544,7 @@ def main():
     # tokens with a non-zero weight: the forward leaves the others out and the
     # backward skips them (a weighted token's gO is 2 (O - t) w / (D den) != 0)
     n_act = int((weight != 0).sum().item()) if weight is not None else N
+    work_tflops = tflops * n_act / N
     de_in_gemm = _lib.bwd_tiling(torch.bfloat16, N, K, V, D, args.chunk)["kernel"] == 2
     traffic, fresh = load_traffic()
     per_kernel = {}
@@ -481,8 +559,10 @@ def main():
         if alg is not None:
             per_kernel[name]["algorithmic_bytes_per_launch"] = int(alg)
         if tr is not None:
-            per_kernel[name]["hbm_fetch_bytes_per_launch"] = int(tr[0])
-            per_kernel[name]["hbm_write_bytes_per_launch"] = int(tr[1])
+            # FETCH_SIZE / WRITE_SIZE count the L2's requests to the fabric: Infinity Cache (MALL)
+            # hits are included, so these are L2-miss bytes, an upper bound on DRAM traffic
+            per_kernel[name]["l2_miss_fetch_bytes_per_launch"] = int(tr[0])
+            per_kernel[name]["l2_miss_write_bytes_per_launch"] = int(tr[1])
             per_kernel[name]["fetch_over_algorithmic"] = round(tr[0] / alg, 2) if alg else None
             stream_bytes += (tr[0] + tr[1]) * cnt
             stream_ms += kms
@@ -504,21 +584,28 @@ def main():
                                + (f", z_loss {cfg['z']}" if cfg["z"] else ""),
                    "N": N, "K": K, "V": V, "D": D, "chunk": args.chunk},
         "active_tokens": n_act,
-        "work_tflops": round(flops * n_act / N / (ms * 1e-3) / 1e12, 1),
-        "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
-        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
+        # the FLOPs executed (both passes run over the active tokens only) and their share of the peak;
+        # value / effective_pct_bf16_peak count the workload's 2 N V (4K + 3D) over all N tokens
+        "work_tflops": round(work_tflops, 1),
+        "pct_bf16_peak": round(100 * work_tflops / PEAK_BF16_TFLOPS, 1),
+        "effective_pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 1),
+        "fwd_ms": round(fwd_ms, 3), "fwd_tflops": round(fwd_flops * n_act / N / (fwd_ms * 1e-3) / 1e12, 1),
+        "fwd_effective_tflops": round(fwd_flops / (fwd_ms * 1e-3) / 1e12, 1),
         "peak_gib": round(peak_gib, 3),
-        # HBM rate of the kernels that stream W and E: their counter-measured bytes (FETCH_SIZE +
-        # WRITE_SIZE, calibrated, profiles/readout_traffic.json) over their own time; null when the
-        # counters were taken on other sources
-        "we_stream_gbps": round(stream_bytes / (stream_ms * 1e-3) / 1e9, 1) if stream_ms else None,
+        # fabric rate of the kernels that stream W and E: their counter-measured L2-miss bytes
+        # (FETCH_SIZE + WRITE_SIZE, calibrated, profiles/readout_traffic.json; Infinity Cache hits
+        # included, so an upper bound on DRAM traffic) over their own time; null when the counters
+        # were taken on other sources
+        "we_stream_fabric_gbps": round(stream_bytes / (stream_ms * 1e-3) / 1e9, 1) if stream_ms else None,
         "we_algorithmic_gbps": round(we_bytes / (ms * 1e-3) / 1e9, 1),
         "traffic_source": {"file": "profiles/readout_traffic.json", "source_sha": source_sha(),
                            "measured_sha": traffic.get("source_sha") if traffic else None, "fresh": fresh},
         "kernels": per_kernel,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": int(dom_tr[0] + dom_tr[1]) if dom_tr else None},
+                     "traffic": int(dom_tr[0] + dom_tr[1]) if dom_tr else None,
+                     "traffic_counts": "L2-miss bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated); "
+                                       "Infinity Cache hits included"},
         "fp8": fp8,
         "published_reference_ms": {"A100": {3: 240, 2: 115, 4: 160}.get(args.config),
                                    "H200": {3: 98, 2: 48, 4: 62}.get(args.config)},

@@ -276,7 +276,8 @@ int swvr_mse_loss(int64_t N, int64_t D, const float* O, const float* lse, const 
  * training loops, harnesses that forbid hipMalloc).  No reference
  * counterpart.  The per-workgroup partial sums go to a fixed array in device
  * memory that each GPU the library runs on holds until the process ends
- * (8 * ceil(N / 16) bytes used, 2 MiB in all), so N is at most
+ * (8 * ceil(N / 16) bytes used, 2 MiB in all; the array of the stream's
+ * device, the current device's for the null stream), so N is at most
  * SWVR_MSE_NOALLOC_MAX_N; larger N returns SWVR_EINVAL.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (several streams or
  * threads at once) race and must be serialised by the caller.  Each call

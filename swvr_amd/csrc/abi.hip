@@ -665,7 +665,7 @@ int swvr_mse_loss_noalloc(int64_t N, int64_t D, const float* O, const float* lse
   void* ws = nullptr;
   size_t ws_bytes = 0;
   if (N > 0 && reduction != SWVR_REDUCE_NONE) {
-    const hipError_t e = swvr::mse_noalloc_scratch(&ws);
+    const hipError_t e = swvr::mse_noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
     if (e != hipSuccess) return hip_fail(e, "scratch address");
     ws_bytes = swvr::mse_workspace_bytes((int)N);
   }

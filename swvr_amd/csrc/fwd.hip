@@ -5,10 +5,14 @@
 //   * a workgroup owns BM tokens and one of n_split contiguous vocabulary
 //     ranges; it walks that range BV rows at a time;
 //   * per vocabulary tile it forms S^T = W_tile h_tile^T (BV x BM) with MFMA
-//     over the whole hidden size K, double-buffering K slices through LDS;
-//   * the 4 waves form a 2 (vocabulary) x 2 (tokens) grid.  In the S^T layout
-//     each lane holds one token column, so the softmax max/sum over the
-//     vocabulary is a register reduction plus one lane swap;
+//     over the whole hidden size K, streaming K slices of the packed W and h
+//     through an NS-slot LDS ring (3 slots beside the pinned E^T tile for
+//     2-byte dtypes with D <= 128; 4 for fp32, and at D = 256, where E^T
+//     travels through the ring, fwd_stream_kernel);
+//   * the waves form a WV (vocabulary) x WT (tokens) grid: at D <= 64, 8 waves
+//     of 128 vocabulary rows x 64 tokens (2 x 4) over a 256 x 256 tile.  In
+//     the S^T layout each lane holds one token column, so the softmax max/sum
+//     over the vocabulary is a register reduction plus one lane swap;
 //   * every wave keeps its own running (m, l, acc) over its half of each tile
 //     (an independent partial softmax), and P, rounded to the compute dtype as
 //     the reference rounds it (swvr/chunked.py:103, triton_kernels.py:69),

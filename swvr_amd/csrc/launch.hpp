@@ -218,8 +218,9 @@ size_t mse_workspace_bytes(int N);
 // Largest N of the allocation-free loss entry point, whose partial sums live in
 // a fixed device array (loss.hip) instead of the caller's workspace.
 constexpr int kMseNoAllocMaxTokens = 1 << 22;
-// Address of that array on the current device (looked up once per device).
-hipError_t mse_noalloc_scratch(void** ptr);
+// Address of that array on the device of `stream` (the current device for the
+// null stream), looked up once per device.
+hipError_t mse_noalloc_scratch(hipStream_t stream, void** ptr);
 
 // ---------------------------------------------------------------- e4m3 quantisation
 struct QuantParams {

@@ -132,15 +132,25 @@ void* g_scratch_ptr[kMaxDevices] = {};
 
 }  // namespace
 
-hipError_t mse_noalloc_scratch(void** ptr) {
+hipError_t mse_noalloc_scratch(hipStream_t stream, void** ptr) {
+  // the device the kernels will run on: the stream's (the null stream: the current device's)
   int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the array's address on that device, looked up with it current
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // the array on the current device
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
     g_scratch_ptr[dev] = p;

@@ -7,10 +7,13 @@ merged O and lse) its rows of gW, gE, gb and a term of gh whose sum is the
 whole gh.  Pinned against the fp64 closed form (oracle.reference) and against
 the single-call path.
 """
+import math
+
 import pytest
 import torch
 
 import swvr_amd as swvr
+from swvr_amd import _lib
 from swvr_amd import vocab_shard as vs
 from oracle import reference as ref
 
@@ -89,3 +92,61 @@ def test_shard_backward_sums_to_the_whole_gradient():
     got = (gh, torch.cat(gW), torch.cat(gE), torch.cat(gb))
     for a, r in zip(got, want):
         torch.testing.assert_close(a, r, rtol=1e-4, atol=1e-5)
+
+
+def _rel(a, r):
+    a, r = a.detach().double(), r.detach().double().to(a.device)
+    return ((a - r).norm() / r.norm().clamp_min(1e-30)).item()
+
+
+def _cos(a, r):
+    a, r = a.detach().double().flatten(), r.detach().double().to(a.device).flatten()
+    return (a @ r / (a.norm() * r.norm()).clamp_min(1e-300)).item()
+
+
+# (tag, dtype, N, K, V, D, shard bounds, chunk): uneven shards with a partial last chunk, and shards
+# of whole 8192-row chunks over 17 token blocks of 256, so that every scores workgroup of a full chunk
+# walks two or more blocks (the backward's steady-state loop, swvr_bwd_tiling)
+SHARD_CASES = [
+    ("small-f32", torch.float32, 700, 256, 5003, 64, BOUNDS, 1024),
+    ("small-bf16", torch.bfloat16, 700, 256, 5003, 64, BOUNDS, 1024),
+    ("multiblock-bf16", torch.bfloat16, 4096 + 77, 256, 16384 + 300, 64, [0, 8192, 16384 + 300], 8192),
+    ("multiblock-f32", torch.float32, 2048 + 9, 128, 16384, 64, [0, 8192, 16384], 8192),
+]
+
+
+@pytest.mark.parametrize("tag,dtype,N,K,V,D,bounds,chunk", SHARD_CASES, ids=[c[0] for c in SHARD_CASES])
+def test_shard_backward_matches_the_oracle(tag, dtype, N, K, V, D, bounds, chunk):
+    """Each shard's gW, gE, gb rows and the sum of the shards' gh against the fp64 closed form of the
+    whole vocabulary (swvr/reference.py:5-14 differentiated; the reference computes these with
+    swvr/chunked.py:108-151 over the whole vocabulary), at the north-star bars."""
+    h, W, E, b = inputs(N, K, V, D, dtype, seed=5)
+    g = torch.Generator().manual_seed(7)
+    gO = torch.randn(N, D, generator=g, dtype=torch.float64).to("cuda", torch.float32)
+    glse = (0.3 * torch.randn(N, generator=g, dtype=torch.float64)).to("cuda", torch.float32)
+    if tag.startswith("multiblock"):
+        for a, z in zip(bounds[:-1], bounds[1:]):
+            t = _lib.bwd_tiling(dtype, N, K, z - a, D, chunk)
+            assert math.ceil(N / t["BM"]) >= 2 * t["G"], (t, N)
+    O, lse = shard_forward(h, W, E, b, bounds)
+    gh = torch.zeros(N, K, dtype=torch.float64, device="cuda")
+    parts = []
+    for a, z in zip(bounds[:-1], bounds[1:]):
+        s = vs.shard_backward(gO, glse, h, W[a:z], E[a:z], b[a:z], O, lse, chunk_size=chunk)
+        gh += s[0].double()
+        parts.append((a, z, s[1], s[2], s[3]))
+    torch.cuda.synchronize()
+    O_r, lse_r, gh_r, gW_r, gE_r, gb_r = ref.reference_grads_blocked(h, W, E, b, gO, glse, block=1024)
+    lo = dtype != torch.float32
+    tol_out, tol_grad, min_cos = (1e-2, 2e-2, 0.999) if lo else (1e-5, 1e-4, 0.999999)
+    errs = {"O": _rel(O, O_r), "lse": _rel(lse, lse_r), "gh": _rel(gh, gh_r)}
+    cos = {"gh": _cos(gh, gh_r)}
+    for i, (a, z, gW, gE, gb) in enumerate(parts):
+        for n, x, r in (("gW", gW, gW_r[a:z]), ("gE", gE, gE_r[a:z]), ("gb", gb, gb_r[a:z])):
+            assert x.dtype == dtype and torch.isfinite(x).all(), (tag, i, n)
+            errs[f"{n}{i}"], cos[f"{n}{i}"] = _rel(x, r), _cos(x, r)
+    print(tag, {k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
+    assert errs["O"] <= tol_out and errs["lse"] <= tol_out, errs
+    for n in errs:
+        if n not in ("O", "lse"):
+            assert errs[n] <= tol_grad and cos[n] >= min_cos, (tag, n, errs[n], cos[n])
