@@ -505,11 +505,15 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
 // bf16 / f16 with DP <= 64: 256 tokens x 256 vocabulary rows per workgroup of
 // 8 waves (2 token halves x 4 vocabulary quarters, 128 x 64 per wave, 0.75
 // operand reads per MFMA).  The LDS is a 4-slot ring of 32 KB; per token block
-// it carries the nk K-slices of h and W, then three side tiles for the
-// epilogue: E [BV][DP], gO [BM][DP] and gO^T [DP][BM] (tokens in pe_row
-// order).  The side slots stay pinned through the epilogue; the next block's
-// slices then catch up.  The bias sits in registers, LSE / delta in a
-// double-buffered LDS strip.
+// it carries the nk K-slices of h and W, then the side tiles of the epilogue:
+// E [BV][DP], gO [BM][DP] and gO^T [DP][BM] (tokens in pe_row order).
+//   DP = 64: three side stages; their slots stay pinned through the epilogue,
+//   and the next block's slices catch up after it.
+//   DP = 32: E (16 KB, the same for the workgroup's whole walk) is loaded once
+//   into an LDS region of its own, and gO and gO^T (16 KB each) share one side
+//   stage, so three slots stay free through the epilogue and the ring carries
+//   the next block's first slices without a pause.
+// The bias sits in registers, LSE / delta in a double-buffered LDS strip.
 template <class T, int DP>
 struct ScoresRingTile {
   static constexpr int BM = 256, BV = 256, WT = 2, WV = 4, NT = 64 * WT * WV, NS = 4;
@@ -533,12 +537,19 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   static_assert(TE::NI <= L && TG::NI <= L && TGT::NI <= L, "side tiles fit a slot");
   constexpr int FT = WTR / 32, FV = WVR / 32;
   constexpr int DB = DP / 32, DK = DP / 16;
+  // E pinned in its own region, gO and gO^T in one side stage (see above)
+  constexpr bool PIN_E = DP == 32 && !F8;
+  static_assert(!PIN_E || (TG::BYTES + TGT::BYTES == SB && TG::NI + TGT::NI == L), "gO | gO^T fill one stage");
+  constexpr int N_SIDE = PIN_E ? 1 : 3;  // side stages per token block
 
-  __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * 2 * BM * 4 + (F8 ? BV * 8 : 0)];
+  __shared__ __attribute__((aligned(1024)))
+  char smem[NS * SB + 2 * 2 * BM * 4 + (F8 ? BV * 8 : 0) + (PIN_E ? TE::BYTES : 0)];
   float* const sLD = reinterpret_cast<float*>(smem + NS * SB);  // [2 buffers][LSE BM | delta BM]
   // F8: (bias, score factor) of the tile's rows, read in the epilogue (two fewer registers per
   // row block than holding both); the bf16 kernel holds the bias in registers
   float2* const sBM = reinterpret_cast<float2*>(smem + NS * SB + 2 * 2 * BM * 4);
+  // PIN_E: the workgroup's E tile
+  char* const sEpin = smem + NS * SB + 2 * 2 * BM * 4;
 
   const int lane = lane_id(), w = wave_id();
   const int wt = w / C::WV, wv = w % C::WV;
@@ -569,7 +580,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   }
 
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
-  const int per_blk = nk + 3;
+  const int per_blk = nk + N_SIDE;
   const int total = n_blocks * per_blk;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsL = lds0 + NS * SB;
@@ -603,6 +614,14 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
       }
       ta.issue(st, is_sub * kBK);
       tw.issue(st + TA::BYTES, is_sub * kBK);
+    } else if (PIN_E) {
+      // gO in the stage's first half, gO^T in its second
+      TG tg;
+      tg.setup(static_cast<const T*>(p.gOp) + (int64_t)n0 * DP, DP, BM, DP, (int)threadIdx.x + opaque_zero());
+      tg.issue(st, 0);
+      TGT tgt;
+      tgt.setup(static_cast<const T*>(p.gOt) + (int64_t)n0 * DP, BM, DP, BM, (int)threadIdx.x + opaque_zero());
+      tgt.issue(st + TG::BYTES, 0);
     } else if (is_sub == nk) {
       TE te;
       // an opaque thread index: the load offsets are computed here, once per
@@ -628,6 +647,14 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
     }
     is_slot = is_slot == NS - 1 ? 0 : is_slot + 1;
   };
+  if constexpr (PIN_E) {
+    // the E tile, ahead of every stage: the first stage's wait covers it
+    if (total > 0) {
+      TE te;
+      te.setup(static_cast<const T*>(p.Ep) + (int64_t)vg0 * DP, DP, BV, DP);
+      te.issue(lds_addr(sEpin), 0);
+    }
+  }
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue_next();
 
@@ -637,11 +664,14 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   for (int blk = 0; blk < n_blocks; ++blk) {
     const int n0 = (tb_begin + blk) * BM;
     if (blk > 0) {
-      // slice 0 of this block: every wave has finished the previous epilogue,
-      // so its three side slots are free: catch up to NS - 1 stages ahead
+      // slice 0 of this block: every wave has finished the previous epilogue.
+      // DP = 64: its three side slots are free: catch up to NS - 1 stages
+      // ahead.  DP = 32: the ring stayed NS - 1 stages ahead through it.
       ring.template publish_next<L>();
-      issue_next();
-      issue_next();
+      if constexpr (!PIN_E) {
+        issue_next();
+        issue_next();
+      }
     }
 #pragma unroll
     for (int ft = 0; ft < FT; ++ft)
@@ -651,11 +681,18 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
       tile_reduce_f8<L, false>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
     else
       tile_reduce<T, kBK, L>(sacc, ta, tw, smem, SB, ring, nk, wt * WTR, wv * WVR, issue_next);
-    ring.template publish_next<L>();  // E
-    issue_next();                     // the next block's slice 0 into the last slice's slot
-    ring.template publish_next<L>();  // gO
-    ring.template publish_next<L>();  // gO^T
-    const int slot_gt = ring.slot;
+    int slot_gt;
+    if constexpr (PIN_E) {
+      ring.template publish_next<L>();  // gO | gO^T
+      issue_next();                     // the next block's slice 2 into the last slice's slot
+      slot_gt = ring.slot;
+    } else {
+      ring.template publish_next<L>();  // E
+      issue_next();                     // the next block's slice 0 into the last slice's slot
+      ring.template publish_next<L>();  // gO
+      ring.template publish_next<L>();  // gO^T
+      slot_gt = ring.slot;
+    }
 
     TG tgl;  // layout only
     TE tel;
@@ -664,12 +701,13 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
     // opaque_zero), so it is recomputed per block: hoisted out of the block loop
     // the offsets would be spilled, and each reload from scratch waits (vmcnt in
     // order) for every store issued before it.  The side tiles sit in the three
-    // slots before and at the current one.
+    // slots before and at the current one (DP = 32: gO and gO^T in the current
+    // slot, E in its own region).
     auto dp_block = [&](int fv, int ft) {
       const int ln = lane + opaque_zero();
       const int lr = ln & 31;
-      const char* sGe = smem + ((slot_gt + NS - 1) % NS) * SB;
-      const char* sEe = smem + ((slot_gt + NS - 2) % NS) * SB;
+      const char* sGe = PIN_E ? smem + slot_gt * SB : smem + ((slot_gt + NS - 1) % NS) * SB;
+      const char* sEe = PIN_E ? static_cast<const char*>(sEpin) : smem + ((slot_gt + NS - 2) % NS) * SB;
       f32x16_t d = zero16();
 #pragma unroll
       for (int kd = 0; kd < DK; ++kd)
@@ -691,7 +729,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
         const int ln = lane + opaque_zero();
         const int lr = ln & 31;
         const int vl = wv * WVR + fv * 32 + lr;  // tile-local row of this lane
-        const char* sGte = smem + slot_gt * SB;
+        const char* sGte = smem + slot_gt * SB + (PIN_E ? TG::BYTES : 0);
         const float* sLe = sLD + (blk & 1) * (2 * BM);
         const float* sDe = sLe + BM;
         const int tr0 = wt * WTR + ft * 32;  // first token of the block
