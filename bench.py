@@ -6,6 +6,7 @@
     python bench.py --copy-probe-mib 1024  # only a plain device copy (HBM counter calibration)
     python bench.py --mfma-probe         # only the matrix-core probe (the power / clock ceiling)
     python bench.py --library-gemm       # only hipBLASLt (torch.mm) on the gradient GEMMs' shapes
+    python bench.py --reference-table    # only the reference bench's eager vs swvr table (ms, peak GiB)
 
 A step is one forward + backward of the MSE loss (the reference's bench,
 bench/bench.py:30-45) on seeded synthetic inputs already resident in HBM.
@@ -395,6 +396,67 @@ def library_gemm(cfg, chunk, reps=10):
     return {"shape": {"C": C, "Q": Q, "K": K, "active_tokens": n_act}, "real_ds": real, "normal_operands": normal}
 
 
+# The reference bench's shapes (bench/bench.py:14-18): N (tokens per step), K, V, D
+REFERENCE_SHAPES = {"0.6B": (16384, 1024, 151936, 16), "4B": (16384, 2560, 151936, 64),
+                    "8B": (8192, 4096, 128256, 128)}
+
+
+def reference_table(chunks=(8192,), iters=5):
+    """The reference's own benchmark table (bench/bench.py:30-71, README.md:47-53) on this GPU: fwd+bwd
+    time and peak memory of the unweighted MSE loss, the eager formula that materialises the [N, V]
+    logits (bench/bench.py:21-23, run by torch on this GPU) beside swvr_amd, at the reference's three
+    shapes and input draws (h ~ N(0,1), W ~ N(0, 9/K), E ~ N(0,1), bias ~ N(0, 0.25), bf16; target
+    fp32).  Peak memory is measured above the inputs and includes the gradient buffers; 2 untimed
+    steps, then ``iters`` timed ones.  Measurement only: the eager leg is torch's, not the product."""
+    import swvr_amd as swvr
+
+    def eager(h, W, E, b, target, chunk=None):
+        O = torch.softmax(torch.addmm(b, h, W.T).float(), dim=-1) @ E.float()
+        return (O - target).pow(2).mean()
+
+    def ours(h, W, E, b, target, chunk=None):
+        return swvr.softmax_readout_mse(h, W, E, target, b, chunk_size=chunk)
+
+    def measure(fn, inputs, chunk):
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        try:
+            for _ in range(2):
+                fn(*inputs, chunk=chunk).backward()
+            torch.cuda.synchronize()
+            peak = (torch.cuda.max_memory_allocated() - base) / 2**30
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(iters):
+                fn(*inputs, chunk=chunk).backward()
+            t1.record()
+            torch.cuda.synchronize()
+            return t0.elapsed_time(t1) / iters, peak
+        except torch.OutOfMemoryError:
+            return None, None
+        finally:
+            for x in inputs[:4]:
+                x.grad = None
+            torch.cuda.empty_cache()
+
+    rows = []
+    for name, (N, K, V, D) in REFERENCE_SHAPES.items():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        r = lambda *s, sc=1.0: (sc * torch.randn(*s, device="cuda", generator=g)).to(torch.bfloat16)
+        inputs = [r(N, K), r(V, K, sc=3 / K ** 0.5), r(V, D), r(V, sc=0.5)]
+        inputs = [x.requires_grad_(True) for x in inputs] + [torch.randn(N, D, device="cuda")]
+        runs = [("eager", eager, None)] + [(f"swvr_amd C={c}", ours, c) for c in chunks]
+        for label, fn, chunk in runs:
+            ms, gib = measure(fn, inputs, chunk)
+            row = {"shape": name, "N": N, "K": K, "V": V, "D": D, "run": label,
+                   "ms": None if ms is None else round(ms, 2), "peak_gib": None if gib is None else round(gib, 2)}
+            print(json.dumps({"reference_table": row}), flush=True)
+            rows.append(row)
+        del inputs
+    return rows
+
+
 def fp8_path(h, W, E, b, target, weight, z, chunk, params, fwd_flops, flops, iters):
     """The opt-in e4m3 path (swvr_amd.fp8) on the same inputs, reported beside the bf16 line
     (not part of it).  Forward: W quantised once, as a server would keep it; each call quantises
@@ -465,6 +527,9 @@ def main():
                          "counter runs under this directory, and exit")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time torch.mm (hipBLASLt) on the config's gradient GEMM shapes (calibration)")
+    ap.add_argument("--reference-table", action="store_true",
+                    help="run only the reference's own benchmark table (bench/bench.py): eager vs swvr_amd "
+                         "fwd+bwd time and peak memory at its three shapes")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run only the matrix-core probe (swvr_probe_mfma: the bare MFMA step with random, zero "
                          "and LDS-fed operands) and print its rates")
@@ -477,6 +542,9 @@ def main():
         return
     if args.mfma_probe:
         print(json.dumps({"mfma_probe_summary": mfma_probe()}), flush=True)
+        return
+    if args.reference_table:
+        reference_table()
         return
     if args.traffic_from:
         print(json.dumps(traffic_summary(args.traffic_from), indent=1))

@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void bwd_expand_kernel(const float* __restrict
 // ---------------------------------------------------------------- scores
 struct ScoresParams {
   const void* hp;       // h packed in its tiles' LDS image (pack_rows_tiled_kernel)
-  const void* Wp;       // W packed the same way, [V_pad] rows
+  const void* Wp;       // the chunk's W rows packed the same way (its row 0 is row v0 of W)
   int hS;               // reduction slices of both
   const void* Ep;       // packed E [V_pad][DP]
   const float* biasp;   // packed bias [V_pad]
@@ -351,7 +351,7 @@ __global__ __launch_bounds__((ScoresTile<T, DP>::NT)) void bwd_scores_kernel(Sco
   TA ta;
   ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
-  tw.setup(p.Wp, vg0, p.hS);
+  tw.setup(p.Wp, vl0, p.hS);
   // issue cursor: the next stage to load (NS - 1 ahead of the compute)
   int is_blk = 0, is_kt = 0, is_slot = 0;
   auto issue_next = [&]() {
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(512) void bwd_scores_ring_kernel(ScoresParams p) {
   TA ta;
   ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
-  tw.setup(p.Wp, vg0, p.hS);
+  tw.setup(p.Wp, vl0, p.hS);
   const rsrc_t r_none = make_rsrc(nullptr);
   // issue cursor over the walk: stage `issued` is (block is_blk, sub-stage
   // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk, nk+1, nk+2
@@ -872,7 +872,7 @@ __global__ __launch_bounds__(512) void bwd_scores_wide_kernel(ScoresParams p) {
   TA ta;
   ta.setup(p.hp, tb_begin * BM, p.hS);
   TB tw;
-  tw.setup(p.Wp, vg0, p.hS);
+  tw.setup(p.Wp, vl0, p.hS);
   const T* const gOp = static_cast<const T*>(p.gOp);
   TG tg;
   tg.setup(gOp + (int64_t)tb_begin * BM * DP, DP, BM, DP);
@@ -1048,8 +1048,9 @@ struct GemmParams {
   int64_t N_pad;
   const void* h;   // h rows in position order
   int64_t ldh;
-  const void* W;
+  const void* W;   // W rows from row w_row0 on, row-major
   int64_t ldw;
+  int w_row0;
   int N, K;
   int v0, cv;
   int n_n;         // tiles along K
@@ -1357,7 +1358,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
     StageBRLoader<T, GM, kBK, NT> ta;
     ta.setup(p.stage, mt * GM, p.n_tb32);
     RTile<T, GN, kBK, NT> tb;
-    tb.setup(static_cast<const T*>(p.W) + (int64_t)p.v0 * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);
+    tb.setup(static_cast<const T*>(p.W) + (int64_t)(p.v0 - p.w_row0) * p.ldw + nt * GN, p.ldw, p.K - nt * GN, p.cv);
     gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, p.cv, wm * (GM / G::WM), wn * (GN / G::WN));
   }
   const int rows = DW ? p.cv : p.N;
@@ -1600,10 +1601,11 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
   int* n_act = reinterpret_cast<int*>(ws + plan.off_nact);
   float* delta = reinterpret_cast<float*>(ws + plan.off_delta);
   T* hc = reinterpret_cast<T*>(ws + plan.off_hc);
-  // W in the compute dtype, row-major: the caller's, or a copy made while packing an fp32 W
+  // W in the compute dtype, row-major, as the dh product reads it: the caller's, or for an fp32 W
+  // a copy made while packing, chunk c's rows in buffer c % 2 (the launch that reads chunk c
+  // writes chunk c + 1's rows)
   T* Wc = (sizeof(T) == 2 && p.w_f32) ? reinterpret_cast<T*>(ws + plan.off_Wc) : nullptr;
-  const void* Wr = Wc ? static_cast<const void*>(Wc) : p.W;
-  const int64_t ldwr = Wc ? p.K : p.ldw;
+  auto wc_buf = [&](int c) { return Wc + (int64_t)(c & 1) * plan.C * p.K; };
   // e4m3 scores: e4m3 h over positions (bytes, read as K8 / 2 pairs) and the per-row multipliers
   const bool f8 = p.hq != nullptr;
   T* hqc = reinterpret_cast<T*>(ws + plan.off_hqc);
@@ -1656,12 +1658,14 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     } else {
       if ((e = launch_pack_rows<T>(hc, p.K, (int)plan.N_pad, p.K, plan.hS, plan.N_pad, hp, stream)) != hipSuccess)
         return e;
-      // fp32 W: the packing also writes the row-major copy the dh product reads.  When every
-      // chunk has a gradient GEMM launch, chunk c + 1's rows are packed by chunk c's launch
-      // (gemm_pack_w), so only the first chunk's are packed here.
-      const int64_t rows0 = fold_pack ? (p.V < plan.C ? p.V : plan.C) : p.V;
-      const int64_t pad0 = fold_pack ? (rows0 + plan.BV - 1) / plan.BV * plan.BV : plan.V_pad;
-      if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, (int)rows0, p.K, plan.hS, pad0, Wp, stream, Wc)) != hipSuccess)
+      // Wp holds one chunk's packed rows: the first chunk's are packed here; chunk c + 1's by
+      // chunk c's gradient GEMM launch (gemm_pack_w) after chunk c's scores kernel has read its
+      // own, or, without gradient GEMM launches, before chunk c + 1's scores kernel.  fp32 W: the
+      // packing also writes the row-major copy the dh product reads.
+      const int64_t rows0 = p.V < plan.C ? p.V : plan.C;
+      const int64_t pad0 = (rows0 + plan.BV - 1) / plan.BV * plan.BV;
+      if ((e = pack_src<T>(p.W, p.w_f32, p.ldw, (int)rows0, p.K, plan.hS, pad0, Wp, stream,
+                           fold_pack ? Wc : nullptr)) != hipSuccess)
         return e;
     }
     timing_end(kKindPack, stream);
@@ -1680,9 +1684,17 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
     if ((int64_t)Gc * Cc > (int64_t)plan.G * plan.C) Gc = (int)((int64_t)plan.G * plan.C / Cc);
     if (Gc < plan.G) Gc = plan.G;  // a full chunk: the plan's G
     const int n_gpart_c = plan.n_gpart / plan.G * Gc;
+    if (!f8 && !fold_pack && c > 0) {
+      timing_begin(kKindPack, stream);
+      e = pack_src<T>(static_cast<const char*>(p.W) + (int64_t)v0 * p.ldw * (p.w_f32 ? 4 : (int64_t)sizeof(T)),
+                      p.w_f32, p.ldw, cv, p.K, plan.hS, Cc, Wp, stream, nullptr);
+      timing_end(kKindPack, stream);
+      if (e != hipSuccess) return e;
+    }
     ScoresParams sp;
     sp.hp = hp;
-    sp.Wp = Wp;
+    // e4m3: Wp holds every row's packed image; the kernels address the chunk's rows from row v0
+    sp.Wp = f8 ? Wp + (int64_t)v0 * plan.hS8 * SliceK<T>::value : Wp;
     sp.hS = f8 ? plan.hS8 : plan.hS;
     sp.Ep = Ep;
     sp.biasp = biasp;
@@ -1720,8 +1732,9 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.N_pad = plan.N_pad;
       gp.h = hc;
       gp.ldh = p.K;
-      gp.W = Wr;
-      gp.ldw = ldwr;
+      gp.W = Wc ? static_cast<const void*>(wc_buf(c)) : p.W;
+      gp.ldw = Wc ? p.K : p.ldw;
+      gp.w_row0 = Wc ? v0 : 0;
       gp.N = p.N;
       gp.K = p.K;
       gp.v0 = v0;
@@ -1768,8 +1781,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
         gp.pk_ld = p.ldw;
         gp.pk_rows = cv1;
         gp.pk_S = plan.hS;
-        gp.pk_dst = Wp + v1 * plan.hS * SliceK<T>::value;
-        gp.pk_rowmajor = Wc ? Wc + v1 * p.K : nullptr;
+        gp.pk_dst = Wp;
+        gp.pk_rowmajor = Wc ? wc_buf(c + 1) : nullptr;
         gp.n_pack_tiles = (pad1 / 32) * ((plan.hS + 7) / 8);
         const int iters = (gp.n_pack_tiles + H - 1) / H;
         gp.n_pack = iters < 1024 ? iters : 1024;
@@ -1918,8 +1931,9 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   const int hs_max = plan->hS > plan->hS8 ? plan->hS : plan->hS8;
   plan->off_hp = off;
   off += align256((size_t)plan->N_pad * hs_max * bk * tb);
+  // packed W: one chunk's rows (the e4m3 scores: every row's, packed once)
   plan->off_Wp = off;
-  off += align256((size_t)plan->V_pad * hs_max * bk * tb);
+  off += align256((size_t)(K8 > 0 ? plan->V_pad : c) * hs_max * bk * tb);
   plan->off_flag = off;
   off += align256((size_t)plan->N_pad * 4);
   plan->off_idx = off;
@@ -1932,8 +1946,9 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   off += align256((size_t)plan->N_pad * 4);
   plan->off_hc = off;
   off += align256((size_t)plan->N_pad * K * tb);
+  // fp32 W: its compute-dtype rows of two chunks (one when there is one chunk)
   plan->off_Wc = off;
-  if (w_f32 && tb == 2) off += align256((size_t)V * K * tb);
+  if (w_f32 && tb == 2) off += align256((size_t)(plan->n_chunks > 1 ? 2 : 1) * c * K * tb);
   plan->off_hqc = off;  // e4m3 h over positions, K8 bytes per row
   if (K8 > 0) off += align256((size_t)plan->N_pad * K8);
   plan->off_mult = off;

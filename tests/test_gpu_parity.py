@@ -82,6 +82,30 @@ def test_autocast_with_fp32_params():
         assert rel_err(a, r) < 2e-2
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.bfloat16, 200), (torch.float32, 16)])
+def test_frozen_h_and_W_over_several_chunks(dtype, D):
+    """Only E and the bias train, over five chunks (the last partial).  Without gh and gW the narrow
+    and fp32 scores kernels' chunks have no gradient GEMM launch, so each chunk's W rows are packed
+    into the one-chunk buffer just before its scores kernel; the wide kernel's chunks keep their
+    launch (it forms dE), which packs the next chunk's rows."""
+    N, K, V = 300, 256, 5003
+    h, W, E, b = make(N, K, V, D, dtype)
+    h.requires_grad_(False)
+    W.requires_grad_(False)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    gO = torch.randn(N, D, device="cuda", generator=g)
+    glse = 0.1 * torch.randn(N, device="cuda", generator=g)
+    out = run(lambda *a: swvr.softmax_readout(*a, chunk_size=1024), (h, W, E, b), gO, glse)
+    want = oracle_run((h, W, E, b), gO, glse)
+    assert len(out) == 4
+    low = dtype != torch.float32
+    for name, a, r in zip(["O", "lse", "gE", "gb"], out, want):
+        e = rel_err(a, r)
+        assert e < ((1e-2 if name in ("O", "lse") else 2e-2) if low else 1e-4), (name, e)
+        if low and name in ("gE", "gb"):
+            assert cosine(a, r) >= 0.999, name
+
+
 def test_bf16_chunk_invariance():
     inputs = make(300, 256, 9000, 16, torch.bfloat16)
     gO, glse = torch.randn(300, 16, device="cuda"), torch.randn(300, device="cuda")

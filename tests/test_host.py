@@ -47,10 +47,13 @@ def test_workspace_sizes():
     fwd = lib.swvr_fwd_workspace_size(_lib.BF16, N, K, V, D)
     assert 0 < fwd < 2**30
     bwd = lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 8192, 1)
-    # dS stage (N x 8192 bf16) + fp32 dh accumulator + packed h and W and the position-ordered
-    # h (bf16) + small partials: O(N * chunk + (N + V) * K)
-    need = N * 8192 * 2 + N * K * 4 + (2 * N + V) * K * 2
+    # dS stage (N x 8192 bf16) + fp32 dh accumulator + packed h, the position-ordered h (bf16) and
+    # one chunk's packed W rows + small partials: O(N * chunk + (N + chunk) * K)
+    need = N * 8192 * 2 + N * K * 4 + (2 * N + 8192) * K * 2
     assert need <= bwd < need + 2**27
+    # per vocabulary row only the packed E row (DP = 64) and the bias remain
+    grow = lib.swvr_bwd_workspace_size(_lib.BF16, N, K, 2 * V, D, 8192, 1) - bwd
+    assert 0 < grow <= V * (64 * 2 + 4) + 2 * 256
     assert lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 0, 1) == 0
     # a forward wider than one pass (256; fp32 128) reuses one pass's workspace for every slice
     assert lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 300) == lib.swvr_fwd_workspace_size(_lib.F32, N, K, V, 128)
@@ -100,12 +103,14 @@ def test_abi_mixed_storage_dtypes_are_checked():
     assert b"h dtype" in lib.swvr_last_error()
     assert lib.swvr_fwd_mixed(_lib.F16, _lib.F16, _lib.BF16, *args) == _lib.EDTYPE
     assert b"W dtype" in lib.swvr_last_error()
-    # an fp32 W adds its compute-dtype copy to the backward workspace
+    # an fp32 W adds the compute-dtype copy of two chunks' rows to the backward workspace
     N, K, V, D = 1024, 512, 4096, 64
     same = lib.swvr_bwd_workspace_size_mixed(_lib.BF16, _lib.BF16, N, K, V, D, 1024, 1)
     f32w = lib.swvr_bwd_workspace_size_mixed(_lib.BF16, _lib.F32, N, K, V, D, 1024, 1)
     assert same == lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, 1024, 1)
-    assert f32w - same == V * K * 2
+    assert f32w - same == 2 * 1024 * K * 2
+    one = lib.swvr_bwd_workspace_size_mixed(_lib.BF16, _lib.F32, N, K, V, D, V, 1)  # one chunk
+    assert one - lib.swvr_bwd_workspace_size(_lib.BF16, N, K, V, D, V, 1) == V * K * 2
 
 
 def test_abi_bwd_rejects_bad_chunk_and_gradient_dtype():
