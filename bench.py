@@ -267,7 +267,8 @@ def mfma_probe(iters=1 << 20, launches=3):
     step (6, 4 or 3 reads per 8 MFMAs), the 6 reads in the hot loops' software-pipelined order,
     4 LDS reads with the B operands loaded from an L2-resident array into registers, and the hot
     loops' whole step (pipelined reads, a barrier and 32 KB of direct-to-LDS stage loads every 2
-    steps).  The launches of a mode run back to back; the rate is the mean over them."""
+    steps), and that step with the barrier and 64 KB of stage loads every 4 steps (two slices per
+    stage).  The launches of a mode run back to back; the rate is the mean over them."""
     from swvr_amd import _lib
     lib = _lib.load()
     wgs = 256
@@ -276,7 +277,8 @@ def mfma_probe(iters=1 << 20, launches=3):
     res = {}
     for mode, name in ((0, "random_registers"), (1, "zero_registers"), (2, "random_lds"),
                        (3, "random_lds_4_reads"), (4, "random_lds_3_reads"), (5, "random_lds_pipelined"),
-                       (6, "random_lds_4_reads_b_from_l2"), (7, "random_lds_pipelined_stage_loads_barriers")):
+                       (6, "random_lds_4_reads_b_from_l2"), (7, "random_lds_pipelined_stage_loads_barriers"),
+                       (8, "random_lds_pipelined_stage_loads_barrier_per_4_steps")):
         _lib.check(lib.swvr_probe_mfma(wgs, 1 << 14, mode, _lib.ptr(out), _lib.stream_of(out.device)))
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -297,7 +297,9 @@ int swvr_mse_loss_noalloc(int64_t N, int64_t D, const float* O, const float* lse
  * order, 6: A from LDS (4 reads per 8 MFMAs) and B loaded from an L2-resident device array into
  * registers 8 steps ahead (iters rounded up to a multiple of 8), 7: as 5 with a workgroup barrier
  * and 32 KB of direct-to-LDS stage loads every 2 steps, the hot loops' whole step (iters rounded up
- * to a multiple of 2).  out receives workgroups * 512 floats (the accumulator sums).
+ * to a multiple of 2), 8: as 7 with the barrier and 64 KB of stage loads every 4 steps (two slices
+ * per stage; iters rounded up to a multiple of 4).  out receives workgroups * 512 floats (the
+ * accumulator sums).
  * Timed, it measures the rate the chip sustains for such data. */
 int swvr_probe_mfma(int64_t workgroups, int64_t iters, int mode, float* out, void* stream);
 

@@ -566,8 +566,8 @@ int swvr_bwd_f64(int64_t N, int64_t K, int64_t V, int64_t D, const double* h, in
 
 int swvr_probe_mfma(int64_t workgroups, int64_t iters, int mode, float* out, void* stream) {
   g_err[0] = 0;
-  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 24) || mode < 0 || mode > 7)
-    return fail(SWVR_EINVAL, "probe: workgroups in [1, 2^20], iters in [1, 2^24], mode 0 to 7");
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 24) || mode < 0 || mode > 8)
+    return fail(SWVR_EINVAL, "probe: workgroups in [1, 2^20], iters in [1, 2^24], mode 0 to 8");
   if (!out) return fail(SWVR_EINVAL, "out must be non-null");
   hipError_t e = swvr::probe_mfma((int)workgroups, (int)iters, mode, out, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "probe launch");

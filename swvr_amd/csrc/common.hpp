@@ -724,6 +724,53 @@ __device__ __forceinline__ void tile_reduce(f32x16_t (&acc)[FM][FN], const TA& t
   }
 }
 
+// tile_reduce over stages that each hold P consecutive slices (slice s of a
+// stage at byte s * sb1 of its slot, A then B as in a one-slice stage): one
+// wait + barrier per P slices.  nst stages; a stage past the last slice holds
+// zeros (its products add nothing).
+template <class T, int BK, int P, int L, int FM, int FN, class TA, class TB, class R, class F>
+__device__ __forceinline__ void tile_reduce_multi(f32x16_t (&acc)[FM][FN], const TA& ta, const TB& tb,
+                                                  const char* smem, int sb, int sb1, R& ring, int nst, int a_row0,
+                                                  int b_row0, F&& issue_next) {
+  constexpr int J1 = BK / 16, J = P * J1;
+  OpOffsets<typename TA::Layout, FM, J1> ao;
+  ao.init(a_row0);
+  OpOffsets<typename TB::Layout, FN, J1> bo;
+  bo.init(b_row0);
+  StepOps<T, FM, FN> cur, nxt;
+  {
+    const char* sA = smem + ring.slot * sb;
+    load_step(cur, ao, bo, sA, sA + TA::BYTES, 0);
+  }
+  for (int kt = 0; kt + 1 < nst; ++kt) {
+    const char* st = smem + ring.slot * sb;
+    issue_next();
+#pragma unroll
+    for (int j = 0; j + 1 < J; ++j) {
+      const char* sA = st + ((j + 1) / J1) * sb1;
+      mma_load_step(acc, cur, nxt, ao, bo, sA, sA + TA::BYTES, (j + 1) % J1);
+      cur = nxt;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    ring.template publish_next<L>();
+    __builtin_amdgcn_sched_barrier(0);
+    const char* nA = smem + ring.slot * sb;
+    mma_load_step(acc, cur, nxt, ao, bo, nA, nA + TA::BYTES, 0);
+    cur = nxt;
+  }
+  {
+    const char* st = smem + ring.slot * sb;
+    issue_next();
+#pragma unroll
+    for (int j = 0; j + 1 < J; ++j) {
+      const char* sA = st + ((j + 1) / J1) * sb1;
+      mma_load_step(acc, cur, nxt, ao, bo, sA, sA + TA::BYTES, (j + 1) % J1);
+      cur = nxt;
+    }
+    mma_step(acc, cur);
+  }
+}
+
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 

@@ -321,30 +321,37 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
 }
 
 // Forward for D = 256 (2-byte dtypes): E^T is not pinned in LDS.  Per
-// vocabulary tile the ring carries the nk K-slices of W and h (-> S^T), then
-// the 8 D-slices of the tile's packed E^T (32 x BV each, 16 KB, one stage
-// slot each), so the LDS holds only the ring: 256 vocabulary rows x 128
-// tokens per workgroup of 8 waves (2 vocabulary halves x 4 token quarters,
-// 128 x 32 each), twice the tile the pinned 64 KB E^T tile left room for
-// (85 flop per byte of operand traffic instead of 64).  The bias of a tile
-// is loaded with its first K-slice into a double-buffered strip.
+// vocabulary tile the ring carries the K-slices of W and h (-> S^T), then the
+// 8 D-slices of the tile's packed E^T (32 x BV each, 16 KB), so the LDS holds
+// only the ring: 256 vocabulary rows x 128 tokens per workgroup of 8 waves
+// (2 vocabulary halves x 4 token quarters, 128 x 32 each), twice the tile the
+// pinned 64 KB E^T tile left room for (85 flop per byte of operand traffic
+// instead of 64).  Each of the ring's 3 stages holds two slices (48 KB: two
+// K-slices, or two D-slices), so the wait + barrier that publishes a stage
+// comes once per 128 MFMAs of the workgroup, as in the 256 x 256 tile of the
+// narrow forward.  The bias of a tile is loaded with its first K-slices into a
+// double-buffered strip.
 template <class T, int DP>
 __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdParams p) {
   typedef FwdTile<T, DP> C;
   typedef typename Vec8<T>::type V8;
   constexpr int kBK = SliceK<T>::value;
-  constexpr int BV = C::BV, BM = C::BM, NT = C::NT, NS = C::NS;
+  constexpr int BV = C::BV, BM = C::BM, NT = C::NT;
+  constexpr int NS = 3, P = 2;  // ring stages, slices per stage
   constexpr int WVR = BV / C::WV, WTR = BM / C::WT;  // rows per wave
   typedef PackedKLoader<T, BV, kBK, NT> TA;  // W rows of the vocabulary tile (packed)
   typedef PackedKLoader<T, BM, kBK, NT> TB;  // h rows of the token block (packed)
   constexpr int DS = 32;                     // E^T rows (embedding columns) per D-slice
   typedef KTile<T, DS, BV, NT> TE;           // one D-slice of the packed E^T tile, pe_row order
-  constexpr int SB = TA::BYTES + TB::BYTES;
-  constexpr int L = TA::NI + TB::NI;         // loads per thread per stage (E stages padded to it)
-  static_assert(sizeof(T) == 2 && DP % DS == 0 && TE::BYTES <= SB && TE::NI <= L, "E^T slices fit a stage");
+  constexpr int SB1 = TA::BYTES + TB::BYTES; // one slice
+  constexpr int SB = P * SB1;                // one stage
+  constexpr int L1 = TA::NI + TB::NI;        // loads per thread per slice (E^T slices padded to it)
+  constexpr int L = P * L1;                  // per stage
+  static_assert(sizeof(T) == 2 && DP % (DS * P) == 0 && TE::BYTES <= SB1 && TE::NI <= L1, "E^T slices fit");
+  static_assert(L1 * NT * 16 == SB1, "a slice's loads fill its bytes");
   static_assert(!TA::PARTIAL && !TB::PARTIAL && !TE::PARTIAL, "whole loads");
   constexpr int FV = WVR / 32, FT = WTR / 32;  // 32x32 blocks per wave
-  constexpr int DB = DP / 32, ND = DP / DS;
+  constexpr int DB = DP / 32, ND = DP / DS, NE = ND / P;
 
   __shared__ __attribute__((aligned(1024))) char smem[NS * SB + 2 * BV * 4];
   const float* const sBias = reinterpret_cast<const float*>(smem + NS * SB);  // [2][BV]
@@ -376,8 +383,9 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
   }
 
   const int nk = max(1, (p.K + kBK - 1) / kBK);  // K = 0: one all-zero slice (bias-only scores)
+  const int nkst = (nk + P - 1) / P;             // K-stages per tile; an odd nk leaves a zero slice
   const int n_tiles = vt_end - vt_begin;
-  const int per_tile = nk + ND;
+  const int per_tile = nkst + NE;
   const int total = n_tiles * per_tile;
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ldsB = lds0 + NS * SB;
@@ -388,28 +396,47 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
   TE te;
   te.setup(Ep, BV, DS, BV);
   const rsrc_t r_none = make_rsrc(nullptr);
+  auto zero_fill = [&](int from, uint32_t st) {  // zero-filling loads from..L1-1 of a slice
+#pragma unroll
+    for (int i = 0; i < L1; ++i)
+      if (i >= from) dma_batch1(r_none, kOOB, st + i * NT * 16 + w * 1024);
+  };
   // issue cursor over the walk: stage `issued` is (tile is_tile, sub-stage
-  // is_sub) into slot is_slot; sub-stages 0..nk-1 are K-slices, nk.. the D-slices of E^T
+  // is_sub) into slot is_slot; sub-stages 0..nkst-1 hold K-slices 2 sub and
+  // 2 sub + 1, nkst.. D-slices 2 e and 2 e + 1 of the tile's E^T
   int issued = 0, is_tile = 0, is_sub = 0, is_slot = 0;
   auto issue_next = [&]() {
     if (issued >= total) return;
     const uint32_t st = lds0 + is_slot * SB;
     const int v0 = (vt_begin + is_tile) * BV;
-    if (is_sub < nk) {
+    if (is_sub < nkst) {
       if (is_sub == 0) {
         ta.rebase(v0);
         // the tile's bias into strip (tile & 1), ahead of its slices (wave 0)
         if ((int)threadIdx.x * 16 < BV * 4)
           dma_batch1(make_rsrc(p.biasp + v0), (uint32_t)threadIdx.x * 16, ldsB + (is_tile & 1) * (BV * 4) + w * 1024);
       }
-      ta.issue(st, is_sub * kBK);
-      tbh.issue(st + TA::BYTES, is_sub * kBK);
-    } else {
-      // rows d0 .. d0 + 31 of the tile's E^T [DP][BV]: one contiguous run
-      te.base = reinterpret_cast<const char*>(Ep + ((int64_t)v0 * DP + (int64_t)(is_sub - nk) * DS * BV));
-      te.issue(st, 0);
 #pragma unroll
-      for (int i = TE::NI; i < L; ++i) dma_batch1(r_none, kOOB, st + i * NT * 16 + w * 1024);
+      for (int s = 0; s < P; ++s) {
+        const int k = P * is_sub + s;
+        const uint32_t ss = st + s * SB1;
+        if (k < nk) {
+          ta.issue(ss, k * kBK);
+          tbh.issue(ss + TA::BYTES, k * kBK);
+        } else {
+          zero_fill(0, ss);
+        }
+      }
+    } else {
+      // rows d0 .. d0 + 31 of the tile's E^T [DP][BV]: one contiguous run per D-slice
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        const int ds = P * (is_sub - nkst) + s;
+        const uint32_t ss = st + s * SB1;
+        te.base = reinterpret_cast<const char*>(Ep + ((int64_t)v0 * DP + (int64_t)ds * DS * BV));
+        te.issue(ss, 0);
+        zero_fill(TE::NI, ss);
+      }
     }
     ++issued;
     if (++is_sub == per_tile) {
@@ -424,14 +451,14 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
   f32x16_t sacc[FV][FT];
   Ring<NS> ring{NS - 1, total};  // the first publish_next() moves to stage 0, slot 0
   for (int tile = 0; tile < n_tiles; ++tile) {
-    // first K-slice of the tile; every wave has also finished the previous
+    // first K-stage of the tile; every wave has also finished the previous
     // tile's E^T slices, and its bias strip is free again
     ring.template publish_next<L>();
 #pragma unroll
     for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) sacc[fv][ft] = zero16();
-    tile_reduce<T, kBK, L>(sacc, ta, tbh, smem, SB, ring, nk, wv * WVR, wt * WTR, issue_next);
+    tile_reduce_multi<T, kBK, P, L>(sacc, ta, tbh, smem, SB, SB1, ring, nkst, wv * WVR, wt * WTR, issue_next);
 
     // ---- scores -> running softmax of this wave's slice of the tile
     const float* sB = sBias + (tile & 1) * BV + opaque_zero();
@@ -479,30 +506,33 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
         for (int r = 0; r < 16; ++r) oacc[db][ft][r] *= alpha;
     }
 
-    // ---- acc^T[d][token] += E^T[d][v] P^T[v][token], one D-slice per stage.
+    // ---- acc^T[d][token] += E^T[d][v] P^T[v][token], two D-slices per stage.
     // Score registers 8c..8c+7 of a block are the B operand of one k16 step;
     // they hold vocabulary rows 16c + 8(t/4) + 4(lane/32) + t%4, which the
     // packed E^T stores contiguously (pe_row): one read per operand.
 #pragma unroll
-    for (int ds = 0; ds < ND; ++ds) {
+    for (int e = 0; e < NE; ++e) {
       ring.template publish_next<L>();
       issue_next();
-      const char* sEe = smem + ring.slot * SB + opaque_zero();
       const int d = lane & 31;
 #pragma unroll
-      for (int fv = 0; fv < FV; ++fv)
+      for (int s = 0; s < P; ++s) {
+        const char* sEe = smem + ring.slot * SB + s * SB1 + opaque_zero();
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int p0 = wv * WVR + fv * 32 + 8 * (2 * c + (lane >> 5));
-          const V8 av = *reinterpret_cast<const V8*>(sEe + TE::elem(d, p0));
+        for (int fv = 0; fv < FV; ++fv)
 #pragma unroll
-          for (int ft = 0; ft < FT; ++ft) {
-            V8 bv;
+          for (int c = 0; c < 2; ++c) {
+            const int p0 = wv * WVR + fv * 32 + 8 * (2 * c + (lane >> 5));
+            const V8 av = *reinterpret_cast<const V8*>(sEe + TE::elem(d, p0));
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[fv][ft][8 * c + tt]);
-            mfma_k16(oacc[ds][ft], av, bv);
+            for (int ft = 0; ft < FT; ++ft) {
+              V8 bv;
+#pragma unroll
+              for (int tt = 0; tt < 8; ++tt) bv[tt] = from_float<T>(sacc[fv][ft][8 * c + tt]);
+              mfma_k16(oacc[P * e + s][ft], av, bv);
+            }
           }
-        }
+      }
     }
   }
 

@@ -20,7 +20,10 @@
 //      and, per 2 steps, 32 KB of direct-to-LDS stage loads (buffer_load ...
 //      lds) from the 2 MB array into a 3-slot ring, waited for as the loops
 //      wait (the stage traffic every LDS-fed loop here carries; iters rounded
-//      up to a multiple of 2).
+//      up to a multiple of 2);
+//   8  as 7 with a barrier every 4 steps and 64 KB of stage loads per 4 steps
+//      into a 2-slot ring (two 32-wide slices per stage: half the barriers per
+//      MFMA; iters rounded up to a multiple of 4).
 // Comparing the rates shows how much of the datasheet peak this chip reaches
 // with the operand data and LDS traffic of the real kernels, i.e. the ceiling
 // that power and clock set for them.
@@ -61,7 +64,7 @@ __global__ __launch_bounds__(256) void probe_fill_kernel(uint32_t seed) {
 template <int MODE>
 __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t seed, float* out) {
   // 32 KB of operands (and, mode 7, a 3-slot ring of 32 KB stages after them)
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[16384 + (MODE == 7 ? 3 * 16384 : 0)];
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[16384 + (MODE == 7 ? 3 * 16384 : MODE == 8 ? 4 * 16384 : 0)];
   const int tid = threadIdx.x, lane = lane_id();
   const uint32_t base = mix32(seed ^ (blockIdx.x * 512u + tid));
   for (int i = tid; i < 16384; i += 512) lds[i] = random_bf16(mix32(seed * 31u + i));
@@ -82,26 +85,28 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t see
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
   const char* lb = reinterpret_cast<const char*>(lds);
   const int wb = wave_id() * 1024;
-  if constexpr (MODE == 7) {
-    // stage s (every 2 steps) = 4 loads per thread of 16 bytes from the array into slot s % 3,
-    // issued 2 stages ahead; before the barrier that ends a stage the next one has landed
+  if constexpr (MODE == 7 || MODE == 8) {
+    // stage s (every SPB steps) = NL loads per thread of 16 bytes from the array into slot s % NSL,
+    // issued NSL - 1 stages ahead; before the barrier that ends a stage the next one has landed
+    constexpr int SPB = MODE == 7 ? 2 : 4, NSL = MODE == 7 ? 3 : 2, NL = 2 * SPB;
+    constexpr uint32_t SLOT = NL * 8192u;
     const rsrc_t rs = make_rsrc(g_probe_src);
     const uint32_t ring = lds_addr(lds + 16384);
     auto stage_load = [&](int st) {
-      const uint32_t slot = ring + (uint32_t)(st % 3) * 32768u;
+      const uint32_t slot = ring + (uint32_t)(st % NSL) * SLOT;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dma_batch1(rs, ((uint32_t)st * 32768u + (uint32_t)i * 8192u + (uint32_t)threadIdx.x * 16u) &
+      for (int i = 0; i < NL; ++i)
+        dma_batch1(rs, ((uint32_t)st * SLOT + (uint32_t)i * 8192u + (uint32_t)threadIdx.x * 16u) &
                            (2u * kProbeSrc - 1u),
                    slot + (uint32_t)i * 8192u + (uint32_t)wave_id() * 1024u);
     };
-    stage_load(0);
-    stage_load(1);
-    bf16x8_t na[4], nb[2];
-    for (int it = 0; it < iters; it += 2) {
-      stage_load(it / 2 + 2);
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+    for (int st = 0; st < NSL - 1; ++st) stage_load(st);
+    bf16x8_t na[4], nb[2];
+    for (int it = 0; it < iters; it += SPB) {
+      stage_load(it / SPB + NSL - 1);
+#pragma unroll
+      for (int s2 = 0; s2 < SPB; ++s2) {
         const char* win = lb + ((it + s2 + 1) & 3) * 8192 + lane * 16;
 #pragma unroll
         for (int f = 0; f < 2; ++f) nb[f] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + (4 + f) * 1024) & 8191));
@@ -112,9 +117,9 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t see
           na[i] = *reinterpret_cast<const bf16x8_t*>(win + ((wb + i * 1024) & 8191));
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (s2 == 1) {
+        if (s2 == SPB - 1) {
           __builtin_amdgcn_sched_barrier(0);
-          wait_vmcnt<4>();  // the next stage has landed; the one after it may stay in flight
+          wait_vmcnt<(NSL - 2) * NL>();  // the next stage has landed; any after it may stay in flight
           stage_barrier();
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, uint32_t see
 }  // namespace
 
 hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream_t stream) {
-  if (mode == 6 || mode == 7) {
+  if (mode >= 6) {
     probe_fill_kernel<<<256, 256, 0, stream>>>(0x5eedu);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -223,6 +228,7 @@ hipError_t probe_mfma(int workgroups, int iters, int mode, float* out, hipStream
     case 5: probe_mfma_kernel<5><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     case 6: probe_mfma_kernel<6><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     case 7: probe_mfma_kernel<7><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
+    case 8: probe_mfma_kernel<8><<<workgroups, 512, 0, stream>>>(iters, 0x5eedu, out); break;
     default: return hipErrorInvalidValue;
   }
   timing_end(kKindProbe, stream);

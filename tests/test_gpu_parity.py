@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import swvr_amd as swvr
+from oracle import reference as oracle_ref
 from tests.gpu_util import cosine, make, oracle_run, rel_err, run
 
 pytestmark = pytest.mark.gpu
@@ -104,6 +105,20 @@ def test_frozen_h_and_W_over_several_chunks(dtype, D):
         assert e < ((1e-2 if name in ("O", "lse") else 2e-2) if low else 1e-4), (name, e)
         if low and name in ("gE", "gb"):
             assert cosine(a, r) >= 0.999, name
+
+
+@pytest.mark.parametrize("K", [16, 96, 1000, 4096])
+def test_streamed_embedding_forward_slice_counts(K):
+    """D = 256 runs the forward whose ring stages hold two 32-wide K-slices: K = 16 and 96 (1 and 3
+    slices) leave the last stage's second slice empty, 1000 pads the last slice, 4096 fills every
+    stage.  O and LSE against the fp64 oracle at the bf16 bar."""
+    N, V, D = 300, 3000, 256
+    h, W, E, b = make(N, K, V, D, torch.bfloat16, requires_grad=False)
+    with torch.no_grad():
+        O, lse = swvr.softmax_readout(h, W, E, b)
+    Or, lr = oracle_ref.softmax_readout_reference(*(x.detach().cpu().double() for x in (h, W, E, b)))
+    assert rel_err(O, Or) < 1e-2
+    assert rel_err(lse, lr) < 1e-2
 
 
 def test_bf16_chunk_invariance():
