@@ -7,8 +7,9 @@
 //   * per vocabulary tile it forms S^T = W_tile h_tile^T (BV x BM) with MFMA
 //     over the whole hidden size K, streaming K slices of the packed W and h
 //     through an NS-slot LDS ring (3 slots beside the pinned E^T tile for
-//     2-byte dtypes with D <= 128; 4 for fp32, and at D = 256, where E^T
-//     travels through the ring, fwd_stream_kernel);
+//     2-byte dtypes with D <= 64, 4 for fp32; for 2-byte D of 128 and 256
+//     E^T travels through the ring instead, 3 stages of two slices each,
+//     fwd_stream_kernel);
 //   * the waves form a WV (vocabulary) x WT (tokens) grid: at D <= 64, 8 waves
 //     of 128 vocabulary rows x 64 tokens (2 x 4) over a 256 x 256 tile.  In
 //     the S^T layout each lane holds one token column, so the softmax max/sum
@@ -39,16 +40,17 @@ template <class T, int DP>
 struct FwdTile {
   static constexpr bool wide = sizeof(T) == 2;
   static constexpr bool narrow = wide && DP <= 64;
-  // D = 256 (2-byte dtypes): E^T streamed through the ring in D-slices (fwd_stream_kernel)
-  static constexpr bool stream_e = wide && DP == 256;
-  // 2-byte dtypes: 128 x 64 waves (D <= 64), 64 x 64 (D = 128), 128 x 32 (D = 256, E^T streamed):
-  // the widest whose score and acc^T accumulators fit beside the operands
+  // D = 128 and 256 (2-byte dtypes): E^T streamed through the ring in D-slices (fwd_stream_kernel)
+  static constexpr bool stream_e = wide && (DP == 256 || DP == 128);
+  // 2-byte dtypes: 128 x 64 waves (D <= 64), 128 x 32 (D = 128 and 256, E^T streamed): the widest
+  // whose score and acc^T accumulators fit beside the operands at D = 256; at D = 128 they run
+  // 2% faster than 64 x 64 waves with E^T pinned
   static constexpr int BV = wide ? 256 : 128;
   static constexpr int BM = narrow ? 256 : wide ? 128 : 64;
-  static constexpr int WV = narrow ? 2 : wide ? (DP == 128 ? 4 : 2) : 2;
-  static constexpr int WT = narrow ? 4 : wide ? (DP == 128 ? 2 : 4) : 2;
+  static constexpr int WV = 2;
+  static constexpr int WT = narrow ? 4 : wide ? 4 : 2;
   static constexpr int NT = 64 * WV * WT;
-  static constexpr int NS = narrow || (wide && DP == 128) ? 3 : kStages;  // LDS ring depth (160 KB with E^T)
+  static constexpr int NS = narrow ? 3 : kStages;  // LDS ring depth of fwd_tile_kernel (160 KB with E^T)
 };
 
 // The e4m3 forward (h and W in OCP e4m3, E and P in bf16): one k64 MFMA per
@@ -320,13 +322,13 @@ __global__ __launch_bounds__((FwdCfg<T, DP, F8>::NT)) void fwd_tile_kernel(FwdPa
   }
 }
 
-// Forward for D = 256 (2-byte dtypes): E^T is not pinned in LDS.  Per
+// Forward for D = 128 and 256 (2-byte dtypes): E^T is not pinned in LDS.  Per
 // vocabulary tile the ring carries the K-slices of W and h (-> S^T), then the
-// 8 D-slices of the tile's packed E^T (32 x BV each, 16 KB), so the LDS holds
-// only the ring: 256 vocabulary rows x 128 tokens per workgroup of 8 waves
-// (2 vocabulary halves x 4 token quarters, 128 x 32 each), twice the tile the
-// pinned 64 KB E^T tile left room for (85 flop per byte of operand traffic
-// instead of 64).  Each of the ring's 3 stages holds two slices (48 KB: two
+// DP / 32 D-slices of the tile's packed E^T (32 x BV each, 16 KB), so the LDS
+// holds only the ring: 256 vocabulary rows x 128 tokens per workgroup of 8
+// waves (2 vocabulary halves x 4 token quarters, 128 x 32 each); at D = 256
+// that is twice the tile a pinned E^T tile would leave room for (85 flop per
+// byte of operand traffic instead of 64).  Each of the ring's 3 stages holds two slices (48 KB: two
 // K-slices, or two D-slices), so the wait + barrier that publishes a stage
 // comes once per 128 MFMAs of the workgroup, as in the 256 x 256 tile of the
 // narrow forward.  The bias of a tile is loaded with its first K-slices into a
