@@ -164,8 +164,9 @@ int swvr_bwd(int dtype, int64_t N, int64_t K, int64_t V, int64_t D,
              float* gb, void* workspace, size_t workspace_bytes, void* stream);
 
 /* swvr_bwd with h and W stored in their own dtypes, as swvr_fwd_mixed.  With
- * an fp32 W the workspace also holds a copy of W in the compute dtype (the dh
- * product reads W rows): size it with swvr_bwd_workspace_size_mixed. */
+ * an fp32 W the workspace also holds two chunks' rows of W in the compute
+ * dtype (the dh product reads W rows): size it with
+ * swvr_bwd_workspace_size_mixed. */
 size_t swvr_bwd_workspace_size_mixed(int dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
                                      int64_t chunk, int need_gh);
 int swvr_bwd_mixed(int dtype, int h_dtype, int w_dtype, int64_t N, int64_t K, int64_t V, int64_t D,
