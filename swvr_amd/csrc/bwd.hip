@@ -1061,12 +1061,13 @@ struct GemmParams {
   int dh_first;
   float scale;     // logit scale: the stage holds dS, the products are scale * stage^T h and scale * stage W
   const int* n_act;  // active positions (device): the reduction length of dW, the rows of dh
-  // dE^T = gO^T P over positions (wide scores kernel): n_de tiles, n_de_n of them along the chunk
-  int n_de, n_de_n;
+  // dE^T = gO^T P over positions (wide scores kernel): n_de tiles, n_de_n of them along the chunk,
+  // each the reduction over one of de_split equal runs of the positions
+  int n_de, n_de_n, de_split;
   const void* pstage;  // P, tiled like the dS stage
   const void* gOp;     // gO over positions [N_pad][DP]
   int DP;
-  float* part_dE;      // output dE^T [DP][C], fp32 (the scores kernels' dE partials when n_red > 0)
+  float* part_dE;      // output dE^T partials [de_split][DP][C], fp32 (the scores kernels' dE partials when n_red > 0)
   int C;
   // the chunk's dE / db reduction (reduce_tile), as n_red workgroups after the GEMM tiles, n_red_v of
   // them along the chunk rows; n_red = 0 when the reduction is a launch of its own
@@ -1378,9 +1379,13 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int t, char* smem
   }
 }
 
-// One tile of dE^T = gO^T P over the active positions (wide scores kernel):
-// rows d (A: gO over positions read transposed, in stage position order), columns
-// chunk-local vocabulary rows (B: the P stage), written as fp32 [DP][C].
+// One tile of dE^T = gO^T P over one of de_split runs of the active positions (wide scores
+// kernel): rows d (A: gO over positions read transposed, in stage position order), columns
+// chunk-local vocabulary rows (B: the P stage), written as the run's fp32 partial [DP][C].  The
+// runs are whole 32-position blocks; one past the active positions leaves its partial zero.  The
+// split makes the dE^T work pieces of a tile, so a launch whose dW and dh tiles fill whole rounds
+// of the CUs is not left a round of a few whole dE^T tiles; the partials are summed in run order
+// by the reduction after the launch.
 template <class T>
 __device__ __forceinline__ void gemm_tile_de(const GemmParams& p, int t, char* smem) {
   typedef GemmTile<T> G;
@@ -1389,19 +1394,24 @@ __device__ __forceinline__ void gemm_tile_de(const GemmParams& p, int t, char* s
   constexpr int FM = GM / (32 * G::WM), FN = GN / (32 * G::WN);
   const int w = wave_id();
   const int wm = w / G::WN, wn = w % G::WN;
+  const int run = t % p.de_split;
+  t /= p.de_split;
   const int mt = t / p.n_de_n, nt = t % p.n_de_n;
+  const int kq = (min(p.N, p.n_act[0]) + 31) & ~31;        // active positions, whole blocks
+  const int ks = ((kq + p.de_split - 1) / p.de_split + 31) & ~31;  // positions per run
+  const int k0 = min(kq, run * ks), k1 = min(kq, k0 + ks);
   f32x16_t acc[FM][FN];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = zero16();
   PosRLoader<T, GM, kBK, NT> ta;
-  ta.setup(static_cast<const T*>(p.gOp) + mt * GM, p.DP, p.DP - mt * GM, p.N);
+  ta.setup(static_cast<const T*>(p.gOp) + (int64_t)k0 * p.DP + mt * GM, p.DP, p.DP - mt * GM, p.N - k0);
   StageKLoader<T, GN, kBK, NT> tb;
   tb.setup(p.pstage, nt * GN, p.cv - nt * GN, p.n_tb32);
-  gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, (min(p.N, p.n_act[0]) + 31) & ~31, wm * (GM / G::WM),
-                            wn * (GN / G::WN));
-  gemm_store<G>(acc, 1.f, p.part_dE, nullptr, 0, p.DP, mt * GM, nt * GN, p.C, smem);
+  tb.base += (int64_t)(k0 >> 5) * 1024 * (int)sizeof(T);  // the run's first 32-position block
+  gemm_loop<T, kBK, FM, FN>(acc, ta, tb, smem, k1 - k0, wm * (GM / G::WM), wn * (GN / G::WN));
+  gemm_store<G>(acc, 1.f, p.part_dE + (int64_t)run * p.DP * p.C, nullptr, 0, p.DP, mt * GM, nt * GN, p.C, smem);
 }
 
 // Workgroup w of the W packing riding on a GEMM launch: tiles H i + part for i = w, w + n_pack, ...,
@@ -1743,7 +1753,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.n_dw = p.gW ? ((cv + plan.GM - 1) / plan.GM) * gp.n_n : 0;
       gp.n_dh = p.gh ? ((p.N + plan.GM - 1) / plan.GM) * gp.n_n : 0;
       gp.n_de_n = (cv + plan.GN - 1) / plan.GN;
-      gp.n_de = gemm_de ? ((plan.DP + plan.GM - 1) / plan.GM) * gp.n_de_n : 0;
+      gp.de_split = kDeSplit;
+      gp.n_de = gemm_de ? ((plan.DP + plan.GM - 1) / plan.GM) * gp.n_de_n * kDeSplit : 0;
       gp.pstage = pstage;
       gp.gOp = gOp;
       gp.DP = plan.DP;
@@ -1794,7 +1805,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       const dim3 grid((unsigned)((cv + kRedV - 1) / kRedV),
                       p.gE && p.D > 0 ? (unsigned)((p.D + kRedD - 1) / kRedD) : 1u);
       bwd_reduce_kernel<<<grid, 256, 0, stream>>>(
-          part_dE, part_db, plan.kind == kScoresWide ? 1 : n_gpart_c, n_gpart_c, Cc, plan.DP, v0, cv,
+          part_dE, part_db, plan.kind == kScoresWide ? kDeSplit : n_gpart_c, n_gpart_c, Cc, plan.DP, v0, cv,
           p.D, p.gE, p.gE_dtype, p.gb);
       timing_end(kKindBwdReduce, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1908,7 +1919,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->off_stage = off;
   off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pe = off;
-  off += align256((size_t)(kind == kScoresWide ? 1 : plan->n_gpart) * DP * c * 4);
+  off += align256((size_t)(kind == kScoresWide ? kDeSplit : plan->n_gpart) * DP * c * 4);
   plan->off_pstage = off;
   if (kind == kScoresWide) off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pb = off;

@@ -154,6 +154,9 @@ struct BwdPlan {
 
 // Scores kernels of the backward (BwdPlan::kind).
 enum { kScoresGeneral = 0, kScoresRing = 1, kScoresWide = 2 };
+// With the wide scores kernel, dE^T = gO^T P is formed by the gradient GEMM launch as this many
+// partial sums over equal runs of the active positions (fixed-order sum after the launch).
+constexpr int kDeSplit = 8;
 
 // w_f32: W is stored in fp32 and needs a row-major copy in the compute dtype
 // (the dh product reads W rows directly).
