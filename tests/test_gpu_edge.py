@@ -318,6 +318,28 @@ def test_zero_hidden_size():
     torch.testing.assert_close(lse.double(), torch.logsumexp(bd.double(), 0).expand(N), **TOL)
 
 
+@pytest.mark.parametrize("D", [5, 128, 256])
+def test_zero_hidden_size_bf16_forwards(D):
+    """K = 0 through the C ABI in bf16: the one all-zero reduction slice of the 256 x 256 forward
+    (D = 5) and of the streamed-E^T forward's two-slice stages (D = 128, 256: a zero slice beside
+    it).  Every score is the bias, so O = softmax(b) E."""
+    from swvr_amd import _lib
+    lib = _lib.load()
+    N, V = 70, 700
+    g = torch.Generator().manual_seed(5)
+    E = torch.randn(V, D, generator=g).to(device="cuda", dtype=torch.bfloat16)
+    b = (2.0 * torch.randn(V, generator=g)).to("cuda")
+    O = torch.empty(N, D, device="cuda")
+    lse = torch.empty(N, device="cuda")
+    ws = torch.empty(lib.swvr_fwd_workspace_size(_lib.BF16, N, 0, V, D), dtype=torch.uint8, device="cuda")
+    _lib.check(lib.swvr_fwd(_lib.BF16, N, 0, V, D, None, 0, None, 0, _lib.ptr(E), D, _lib.ptr(b), 1.0,
+                            _lib.ptr(O), _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream_of(O.device)))
+    torch.cuda.synchronize()
+    want = torch.softmax(b.double(), 0) @ E.double()
+    assert rel_err(O, want.expand_as(O)) < 1e-2
+    torch.testing.assert_close(lse.double(), torch.logsumexp(b.double(), 0).expand(N), rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("dtype,N,K,V,D", [
     (torch.bfloat16, 40, 32, 1000, 64), (torch.bfloat16, 300, 32, 3000, 16), (torch.float16, 40, 32, 1000, 200),
     (torch.float32, 40, 16, 1000, 64), (torch.float32, 40, 16, 1000, 128), (torch.bfloat16, 6, 32, 300, 5),

@@ -107,12 +107,13 @@ def test_frozen_h_and_W_over_several_chunks(dtype, D):
             assert cosine(a, r) >= 0.999, name
 
 
+@pytest.mark.parametrize("D", [128, 256])
 @pytest.mark.parametrize("K", [16, 96, 1000, 4096])
-def test_streamed_embedding_forward_slice_counts(K):
-    """D = 256 runs the forward whose ring stages hold two 32-wide K-slices: K = 16 and 96 (1 and 3
-    slices) leave the last stage's second slice empty, 1000 pads the last slice, 4096 fills every
-    stage.  O and LSE against the fp64 oracle at the bf16 bar."""
-    N, V, D = 300, 3000, 256
+def test_streamed_embedding_forward_slice_counts(K, D):
+    """D = 128 and 256 run the forward whose ring stages hold two 32-wide K-slices: K = 16 and 96 (1
+    and 3 slices) leave the last stage's second slice empty, 1000 pads the last slice, 4096 fills
+    every stage.  O and LSE against the fp64 oracle at the bf16 bar."""
+    N, V = 300, 3000
     h, W, E, b = make(N, K, V, D, torch.bfloat16, requires_grad=False)
     with torch.no_grad():
         O, lse = swvr.softmax_readout(h, W, E, b)
