@@ -368,7 +368,9 @@ __global__ __launch_bounds__((FwdTile<T, DP>::NT)) void fwd_stream_kernel(FwdPar
     ntok = n_tb * BM;
   }
   int split, tb;
-  grouped_tile<2>(blockIdx.x, n_split, n_tb, &split, &tb);  // 2 vocabulary splits x 16 token blocks per XCD
+  // per XCD, 2 vocabulary splits x 16 token blocks at D = 256, 1 x 32 at D = 128 (each 1-2% faster
+  // than the other there)
+  grouped_tile<DP == 128 ? 1 : 2>(blockIdx.x, n_split, n_tb, &split, &tb);
   const int n0 = tb * BM;
   const int vt_begin = (int)((int64_t)split * p.n_vt / n_split);
   const int vt_end = (int)((int64_t)(split + 1) * p.n_vt / n_split);
