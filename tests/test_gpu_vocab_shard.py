@@ -35,9 +35,11 @@ def shard_forward(h, W, E, b, bounds):
 BOUNDS = [0, 1200, 2501, 3700, 5003]
 
 
+@pytest.mark.parametrize("D", [64, 128, 200])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 1e-2)])
-def test_shards_combine_to_the_whole_vocabulary(dtype, tol):
-    N, K, V, D = 700, 256, 5003, 64
+def test_shards_combine_to_the_whole_vocabulary(dtype, tol, D):
+    # D = 128 and 200 (bf16) run the streamed-E^T forward for each shard
+    N, K, V = 700, 256, 5003
     h, W, E, b = inputs(N, K, V, D, dtype)
     O, lse = shard_forward(h, W, E, b, BOUNDS)
     O1, lse1 = swvr.softmax_readout(h, W, E, b)
@@ -110,6 +112,7 @@ def _cos(a, r):
 SHARD_CASES = [
     ("small-f32", torch.float32, 700, 256, 5003, 64, BOUNDS, 1024),
     ("small-bf16", torch.bfloat16, 700, 256, 5003, 64, BOUNDS, 1024),
+    ("wide-bf16", torch.bfloat16, 700, 256, 5003, 128, BOUNDS, 1024),  # wide scores kernel, dE^T pieces
     ("multiblock-bf16", torch.bfloat16, 4096 + 77, 256, 16384 + 300, 64, [0, 8192, 16384 + 300], 8192),
     ("multiblock-f32", torch.float32, 2048 + 9, 128, 16384, 64, [0, 8192, 16384], 8192),
 ]
