@@ -1753,8 +1753,8 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       gp.n_dw = p.gW ? ((cv + plan.GM - 1) / plan.GM) * gp.n_n : 0;
       gp.n_dh = p.gh ? ((p.N + plan.GM - 1) / plan.GM) * gp.n_n : 0;
       gp.n_de_n = (cv + plan.GN - 1) / plan.GN;
-      gp.de_split = kDeSplit;
-      gp.n_de = gemm_de ? ((plan.DP + plan.GM - 1) / plan.GM) * gp.n_de_n * kDeSplit : 0;
+      gp.de_split = de_split(plan.N_pad);
+      gp.n_de = gemm_de ? ((plan.DP + plan.GM - 1) / plan.GM) * gp.n_de_n * gp.de_split : 0;
       gp.pstage = pstage;
       gp.gOp = gOp;
       gp.DP = plan.DP;
@@ -1805,7 +1805,7 @@ hipError_t bwd_run(const BwdPlan& plan, const BwdParams& p, hipStream_t stream) 
       const dim3 grid((unsigned)((cv + kRedV - 1) / kRedV),
                       p.gE && p.D > 0 ? (unsigned)((p.D + kRedD - 1) / kRedD) : 1u);
       bwd_reduce_kernel<<<grid, 256, 0, stream>>>(
-          part_dE, part_db, plan.kind == kScoresWide ? kDeSplit : n_gpart_c, n_gpart_c, Cc, plan.DP, v0, cv,
+          part_dE, part_db, plan.kind == kScoresWide ? de_split(plan.N_pad) : n_gpart_c, n_gpart_c, Cc, plan.DP, v0, cv,
           p.D, p.gE, p.gE_dtype, p.gb);
       timing_end(kKindBwdReduce, stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1919,7 +1919,7 @@ bool bwd_plan(int dtype, int64_t N, int64_t K, int64_t V, int64_t D, int64_t chu
   plan->off_stage = off;
   off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pe = off;
-  off += align256((size_t)(kind == kScoresWide ? kDeSplit : plan->n_gpart) * DP * c * 4);
+  off += align256((size_t)(kind == kScoresWide ? de_split(plan->N_pad) : plan->n_gpart) * DP * c * 4);
   plan->off_pstage = off;
   if (kind == kScoresWide) off += align256((size_t)c * (size_t)plan->N_pad * tb);
   plan->off_pb = off;

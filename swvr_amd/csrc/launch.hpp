@@ -154,9 +154,14 @@ struct BwdPlan {
 
 // Scores kernels of the backward (BwdPlan::kind).
 enum { kScoresGeneral = 0, kScoresRing = 1, kScoresWide = 2 };
-// With the wide scores kernel, dE^T = gO^T P is formed by the gradient GEMM launch as this many
-// partial sums over equal runs of the active positions (fixed-order sum after the launch).
+// With the wide scores kernel, dE^T = gO^T P is formed by the gradient GEMM launch as up to this
+// many partial sums over equal runs of the positions (fixed-order sum after the launch): one run
+// per 2048 token rows (64 reduction slices), 1 to kDeSplit (de_split).
 constexpr int kDeSplit = 8;
+inline int de_split(int64_t n_pad) {
+  const int64_t s = n_pad / 2048;
+  return s < 1 ? 1 : s > kDeSplit ? kDeSplit : (int)s;
+}
 
 // w_f32: W is stored in fp32 and needs a row-major copy in the compute dtype
 // (the dh product reads W rows directly).
